@@ -1,0 +1,259 @@
+"""ElasticBit linear benchmark on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-prefill] [--no-cpu]
+
+Headline: decode GEMV, ElasticBit linear 4096->4096,
+fp16 activations M=1, weights N(0,0.02) with 1% x8 outlier columns, compressed
+by ElasticBit.compress at threshold 0.01 (the GPU width search picks b).  One
+step is one fused unpack+dequant+GEMV launch over one weight copy; the copies
+rotate over >= 512 MB so the 256 MB MALL cannot hold them, and the K steps are
+captured into one HIP graph and replayed, timed with HIP events on the stream
+the kernels run on.  value = algorithmic bytes per step / time per step, with
+bytes counted at the storage width: ceil(N*K*b/8) + 4N + 2MK + 2MN.
+
+Also reported (not the headline): the prefill GEMM of configs[3] (4096->14336,
+M=2048) in TFLOP/s, and the oracle's OpenMP CPU GEMV on the host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+FP16_PEAK_TFLOPS = 2516.6      # MI355X dense fp16 MFMA
+MALL_BYTES = 256 << 20
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse_args() -> argparse.Namespace:
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=2000)
+    p.add_argument("--warmup", type=int, default=200)
+    p.add_argument("--prefill-steps", type=int, default=20)
+    p.add_argument("--no-prefill", action="store_true")
+    p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    return p.parse_args()
+
+
+def make_weight(rows: int, cols: int):
+    """configs[1..3] weights: randn*0.02 (seed 0), round(0.01*K) columns x8 (seed 3), fp16."""
+    import torch
+
+    w = torch.randn(rows, cols, generator=torch.Generator().manual_seed(0)) * 0.02
+    idx = torch.randperm(cols, generator=torch.Generator().manual_seed(3))[: round(0.01 * cols)]
+    w[:, idx] *= 8
+    return w.half()
+
+
+def compressed_layer(rows: int, cols: int, threshold: float, calib_rows: int):
+    """Run the real ElasticBit.compress pipeline on one Linear (wrapped, as the
+    root module cannot be replaced) and return the compressed layer."""
+    import torch
+
+    from mlbricks_amd import ElasticBit
+
+    lin = torch.nn.Linear(cols, rows, bias=False)
+    with torch.no_grad():
+        lin.weight.copy_(make_weight(rows, cols).float())
+    model = torch.nn.Sequential(lin).cuda().half().eval()
+    calib = torch.randn(calib_rows, cols, generator=torch.Generator().manual_seed(2)).half()
+    ElasticBit.compress(model, calib, threshold)
+    return model[0]
+
+
+def algorithmic_bytes(rows: int, cols: int, bits: int, M: int) -> int:
+    payload = (rows * cols * bits + 7) // 8 if bits < 16 else 2 * rows * cols
+    scales = 4 * rows if bits < 16 else 0
+    return payload + scales + 2 * M * cols + 2 * M * rows
+
+
+def copies_of(layer, count: int):
+    """`count` independent RuntimeMatrix copies of the layer's canonical storage."""
+    from mlbricks_amd.elasticbit import _native as native
+
+    nm = layer.matrix._native
+    scales, _ = nm._canonical()
+    codes = nm._unpackCodesTorch().cpu().numpy()
+    return [native.RuntimeMatrix._compressSelectedCodes(codes, scales, nm.storageBits, nm.threshold, nm.error)
+            for _ in range(count)]
+
+
+def time_graph(launches, steps: int, warmup: int) -> float:
+    """Capture `steps` launches (cycling over `launches`) into one HIP graph, replay it
+    once untimed, then once between HIP events on the launch stream.  Returns ms."""
+    import torch
+
+    for i in range(warmup):
+        launches[i % len(launches)]()
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(steps):
+                launches[i % len(launches)]()
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        graph.replay()
+        stop.record(stream)
+    stop.synchronize()
+    torch.cuda.synchronize()
+    return float(start.elapsed_time(stop))
+
+
+def bench_gemv(args) -> dict:
+    import torch
+
+    rows = cols = 4096
+    layer = compressed_layer(rows, cols, 0.01, 512)
+    bits = layer.matrix.storageBits
+    per_copy = layer.matrix.executionBytes
+    n_copies = max(2, -(-2 * MALL_BYTES // per_copy) + 1)
+    log(f"gemv 4096x4096: selected b={bits}, {n_copies} copies x {per_copy / 1e6:.1f} MB")
+    mats = copies_of(layer, n_copies)
+    x = torch.randn(1, cols, generator=torch.Generator().manual_seed(1)).half().cuda()
+    outs = [torch.empty(1, rows, dtype=torch.float16, device="cuda") for _ in mats]
+    launches = [lambda m=m, y=y: m.forwardTorch(x, out=y) for m, y in zip(mats, outs)]
+    ms = time_graph(launches, args.steps, args.warmup)
+    per_step_ms = ms / args.steps
+    nbytes = algorithmic_bytes(rows, cols, bits, 1)
+    gbs = nbytes / (per_step_ms * 1e-3) / 1e9
+    log(f"gemv: {per_step_ms * 1e3:.3f} us/step, {gbs:.1f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% HBM)")
+    return {"bits": bits, "ms": ms, "per_step_ms": per_step_ms, "bytes": nbytes, "gbs": gbs,
+            "copies": n_copies, "layer": layer}
+
+
+def bench_prefill(args) -> dict:
+    import torch
+
+    rows, cols, M = 14336, 4096, 2048
+    layer = compressed_layer(rows, cols, 0.01, 512)
+    bits = layer.matrix.storageBits
+    x = torch.randn(M, cols, generator=torch.Generator().manual_seed(1)).half().cuda()
+    y = torch.empty(M, rows, dtype=torch.float16, device="cuda")
+    nm = layer.matrix._native
+    ms = time_graph([lambda: nm.forwardTorch(x, out=y)], args.prefill_steps, 3)
+    per = ms / args.prefill_steps
+    flops = 2.0 * M * rows * cols
+    tflops = flops / (per * 1e-3) / 1e12
+    log(f"prefill 4096->14336 M=2048 b={bits}: {per * 1e3:.1f} us, {tflops:.1f} TFLOP/s "
+        f"({100 * tflops / FP16_PEAK_TFLOPS:.1f}% fp16 MFMA)")
+    return {"workload": "ElasticBit linear 4096->14336, fp16 x M=2048, threshold 0.01 (configs[3])",
+            "bits": bits, "us_per_launch": round(per * 1e3, 2), "tflops": round(tflops, 2),
+            "frac_fp16_mfma_peak": round(tflops / FP16_PEAK_TFLOPS, 4)}
+
+
+def cpu_baseline(layer, seconds: float) -> dict:
+    """The oracle's OpenMP GEMV (fp32 accumulate) over the same matrix and the
+    same algorithmic bytes, on this host's cores (bounded to ~`seconds`)."""
+    import numpy as np
+    import torch
+
+    from oracle import oracle as ora
+
+    nm = layer.matrix._native
+    rows, cols, bits = nm.rows, nm.cols, nm.storageBits
+    scales, payload = nm._canonical()
+    x16 = torch.randn(1, cols, generator=torch.Generator().manual_seed(1)).half().numpy().view(np.uint16)
+    cores = len(os.sched_getaffinity(0))
+    threads = min(cores, 16)
+    ora.gemv_f32_baseline(payload, scales, rows, cols, bits, x16, threads=threads)   # warm-up
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        _, used = ora.gemv_f32_baseline(payload, scales, rows, cols, bits, x16, threads=threads)
+        reps += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= seconds:
+            break
+    per = elapsed / reps
+    gbs = algorithmic_bytes(rows, cols, bits, 1) / per / 1e9
+    log(f"cpu baseline: {per * 1e3:.2f} ms/GEMV on {used} threads ({cores} cores visible): {gbs:.2f} GB/s")
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": int(used), "kind": "port",
+            "sample": f"{reps} full 4096x4096 b={bits} M=1 GEMVs ({elapsed:.1f} s), oracle/eb_oracle.c "
+                      f"ebo_gemv_f32_baseline, OpenMP over rows; {cores} cores visible"}
+
+
+def measured_traffic() -> int | None:
+    """HBM bytes per GEMV launch from the committed rocprofv3 PMC summary, if present."""
+    path = ROOT / "profiles" / "gemv_4096x4096_b10_m1_traffic.md"
+    if not path.exists():
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9]+)", path.read_text())
+    return int(m.group(1)) if m else None
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the ElasticBit path is "
+              "benchmarked on a single MI355X.", file=sys.stderr)
+        return 2
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    import mlbricks_amd.elasticbit._native  # noqa: F401  fail loudly if the HIP library is missing
+
+    g = bench_gemv(args)
+    prefill = None if args.no_prefill else bench_prefill(args)
+    cpu = None if args.no_cpu else cpu_baseline(g["layer"], args.cpu_seconds)
+    achieved = g["bytes"] / (g["per_step_ms"] * 1e-3) / 1e9
+    line = {
+        "metric": "ElasticBit linear GB/s (%HBM peak) at M=1; TFLOP/s (%MFMA peak) at M=2048",
+        "value": round(g["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(g["per_step_ms"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic: BASELINE seeds, weights N(0,0.02) with 1% x8 outlier columns, x N(0,1)",
+        "config": {
+            "workload": "decode GEMV: ElasticBit linear 4096->4096, fp16 x M=1, threshold 0.01 (configs[1])",
+            "storage_bits": g["bits"],
+            "weight_copies_rotated": g["copies"],
+            "bytes_per_step": g["bytes"],
+            "timing": "one HIP graph of `steps` launches, HIP events on the launch stream",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic(),
+        },
+        "cpu_baseline": cpu,
+        "prefill": prefill,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

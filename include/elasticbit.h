@@ -1,0 +1,202 @@
+/*
+ * ElasticBit for MI355X (gfx950) -- C ABI of libelasticbit_hip.so.
+ *
+ * This ABI replaces the pybind11 module mlbricks.elasticbit._C and the torch
+ * op mlbricks_native::elastic_linear_packed of MLBricks.  Each declaration
+ * cites the reference interface it stands in for (paths relative to the
+ * MLBricks repository root; "runtime.cu" is
+ * mlbricks/elasticbit/csrc/elasticbit_runtime.cu).
+ *
+ * Conventions
+ *  - Every int-returning call returns EB_OK (0) or an error status; the
+ *    message is available from eb_last_error() on the calling thread.
+ *    EB_INVALID_ARGUMENT maps to the reference's std::invalid_argument
+ *    (Python ValueError); the others map to std::runtime_error (RuntimeError).
+ *  - Device pointers are plain HIP device addresses; streams are hipStream_t
+ *    passed as void* (NULL = the legacy default stream).  No call synchronises
+ *    the stream it is given, and no call allocates on the forward path.
+ *  - fp16 data is IEEE binary16 bit patterns (uint16_t / void*).
+ *  - An eb_matrix owns its host canonical storage and its device execution
+ *    buffers; callers own x / y / out buffers.
+ */
+#ifndef MLBRICKS_AMD_ELASTICBIT_H
+#define MLBRICKS_AMD_ELASTICBIT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EB_ABI_VERSION 1
+
+enum {
+    EB_OK = 0,
+    EB_INVALID_ARGUMENT = 1, /* std::invalid_argument in the reference */
+    EB_RUNTIME_ERROR = 2,    /* std::runtime_error (file I/O, checksums, no device) */
+    EB_DEVICE_ERROR = 3      /* a HIP call failed (CUDA_CHECK, runtime.cu:26-35) */
+};
+
+enum {
+    EB_POLICY_HARDWARE_NATIVE = 1, /* runtime.cu:253-256 DecodePolicy::HardwareNative */
+    EB_POLICY_FULL_PRECISION = 2   /* DecodePolicy::FullPrecision */
+};
+
+enum { EB_DTYPE_F32 = 0, EB_DTYPE_F16 = 1, EB_DTYPE_BF16 = 2 };
+
+typedef struct eb_matrix eb_matrix;
+
+/* Read-only properties, runtime.cu:1051-1066 (rows, cols, storageBits, ...). */
+typedef struct {
+    int rows;
+    int cols;
+    int storage_bits;
+    int execution_width;
+    int decode_policy;          /* EB_POLICY_* */
+    int device_index;           /* -1 when the matrix has no device copy */
+    uint64_t storage_bytes;     /* canonical payload + fp32 scales */
+    uint64_t execution_bytes;   /* device execution buffers */
+    uint64_t original_bytes;    /* 2 * rows * cols */
+    double threshold;
+    double selected_error;
+    double memory_reduction;
+    char execution_planner[32];
+} eb_props;
+
+/* One analyzer candidate, runtime.cu:272-278 (BitAnalysis) / :438-483. */
+typedef struct {
+    int bits;
+    double hardware_native_error;
+    double full_precision_error;
+    double error;
+    uint64_t storage_bytes;
+    double memory_reduction;
+    int passes;
+} eb_bit_analysis;
+
+/* Backend metadata, runtime.cu:1386-1409 (backend_info_py). */
+typedef struct {
+    int available;              /* a HIP device is present */
+    int device_index;
+    int compute_units;
+    int weight_widths[16];
+    int n_weight_widths;
+    int validated;
+    char device[128];
+    char architecture[64];
+    char activate_dtype[16];
+    char prefill[16];
+    char decode_planner[32];
+    char decode_engine[32];
+    char decode_status[32];
+    char decode_validation[64];
+} eb_backend;
+
+/* Thread-local message of the last failing call on this thread. */
+const char* eb_last_error(void);
+int eb_abi_version(void);
+
+/* ---- analyzer and backend ------------------------------------------------ */
+
+/* _C.analyze, runtime.cu:438-483 (analyze_py; algorithm :280-436).
+ * out14 receives b = 3..16; *selected_index the chosen entry. */
+int eb_analyze(const float* weights, int rows, int cols, const float* calibration,
+               int samples, double threshold, eb_bit_analysis* out14, int* selected_index);
+
+/* _C.backendInfo, runtime.cu:1386-1409. */
+int eb_backend_info(eb_backend* out);
+
+/* ---- factories (RuntimeMatrix static methods, runtime.cu:720-871) --------- */
+
+/* RuntimeMatrix.compress, runtime.cu:720-746: analyze, then pack. */
+int eb_compress(const float* weights, int rows, int cols, const float* calibration,
+                int samples, double threshold, int policy, eb_matrix** out);
+
+/* RuntimeMatrix._compressSelected, runtime.cu:748-776. */
+int eb_compress_selected(const float* weights, int rows, int cols, int selected_bits,
+                         double threshold, double selected_error, int policy, eb_matrix** out);
+
+/* RuntimeMatrix._compressSelectedCodes, runtime.cu:778-808. */
+int eb_compress_selected_codes(const int16_t* codes, const float* scales, int rows, int cols,
+                               int selected_bits, double threshold, double selected_error,
+                               int policy, eb_matrix** out);
+
+/* RuntimeMatrix.load, runtime.cu:810-871 (MLB4 reader). */
+int eb_load(const char* path, int policy, eb_matrix** out);
+
+/* RuntimeMatrix.save, runtime.cu:1024-1049 (MLB4 writer). */
+int eb_save(const eb_matrix* m, const char* path);
+
+/* ~RuntimeMatrix, runtime.cu:716,1370-1383.  NULL is ignored. */
+void eb_destroy(eb_matrix* m);
+
+/* ---- properties and policy ------------------------------------------------ */
+
+/* RuntimeMatrix read-only properties, runtime.cu:1051-1066. */
+int eb_get_props(const eb_matrix* m, eb_props* out);
+
+/* RuntimeMatrix.setDecodePolicy, runtime.cu:975-980. */
+int eb_set_decode_policy(eb_matrix* m, int policy);
+
+/* Canonical storage (the MLB4 body): scales (rows floats, none for b=16) and
+ * payload (storage_bytes - 4*rows bytes).  Either pointer may be NULL. */
+int eb_get_canonical(const eb_matrix* m, float* scales_out, uint8_t* payload_out);
+
+/* ---- host-side compute ----------------------------------------------------- */
+
+/* RuntimeMatrix.dequantize, runtime.cu:967-973: fp16_rn(q*s) as float [rows*cols]. */
+int eb_dequantize_host(const eb_matrix* m, float* out);
+
+/* RuntimeMatrix.forward (numpy), runtime.cu:873-900: one fp32 row [cols] ->
+ * fp32 [rows], synchronous, on the legacy default stream. */
+int eb_forward_host(eb_matrix* m, const float* x, float* y);
+
+/* RuntimeMatrix.benchmark, runtime.cu:933-965: ms per launch (M = 1). */
+int eb_benchmark(eb_matrix* m, const float* x, int iterations, double* ms_per_iteration);
+
+/* ---- device compute (stream-ordered, no allocation) ------------------------ */
+
+/* RuntimeMatrix.forwardTorch, runtime.cu:902-931 (decode, M = 1) and the
+ * prefill route materialize + F.linear, core.py:462-471 (M > 1):
+ *   y[M][rows] = x[M][cols] . W^T (+ bias), fp16 in, fp16 out, fp32 accumulate.
+ * hardwareNative: b <= 10 computes fp16_rn(s_r * sum q*x); b >= 11 and
+ * fullPrecision compute fp16_rn(sum fp16_rn(q*s_r) * x).  bias (may be NULL)
+ * is added as torch does, y = fp16_rn(y + bias).  Any M >= 1. */
+int eb_forward(const eb_matrix* m, const void* x_f16, int64_t M, void* y_f16,
+               const void* bias_f16, void* stream);
+
+/* RuntimeMatrix._materializeTorch, runtime.cu:982-1022: out [rows][cols] fp16
+ * = fp16_rn(q*s) (b = 16: the stored fp16). */
+int eb_materialize_fp16(const eb_matrix* m, void* out_f16, void* stream);
+
+/* Parity probe (no reference counterpart as a call; the reference unpacks
+ * with extract_code_host, runtime.cu:188-206): out [rows][cols] int16 codes
+ * q = u - qmax.  Fails for b = 16. */
+int eb_unpack_codes(const eb_matrix* m, int16_t* out, void* stream);
+
+/* mlbricks_native::elastic_linear_packed, bolt/ops.cpp:1012-1043 and
+ * bolt/ops_cuda.cu:2708-2795: y[M][N] = x . W^T + bias with
+ * W[o][k] = (u - 2^(b-1)) * scales[(o*K + k) / group_size], 2 <= b <= 8.
+ * x / bias / y share x_dtype; scales have scale_dtype (EB_DTYPE_*). */
+int eb_packed_linear(const void* x, int x_dtype, int64_t M, const uint8_t* packed,
+                     const void* scales, int scale_dtype, const void* bias, int bits,
+                     int64_t group_size, int64_t out_features, int64_t in_features,
+                     void* y, void* stream);
+
+/* ---- host codec (the packer inside the RuntimeMatrix constructors) --------- */
+
+/* pack_exact_codes, runtime.cu:150-186.  payload_bytes must equal
+ * ceil(count*bits/8). */
+int eb_host_pack_codes(const int16_t* codes, uint64_t count, int bits, uint8_t* payload,
+                       uint64_t payload_bytes);
+
+/* extract_code_host over every element, runtime.cu:188-206: codes = u - qmax. */
+int eb_host_unpack_codes(const uint8_t* payload, uint64_t payload_bytes, uint64_t count,
+                         int bits, int16_t* codes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,735 @@
+// ElasticBit gfx950 kernels: bit-plane repack, unpack, materialize, the fused
+// unpack + dequant + MFMA linear (decode and prefill), and the legacy
+// flat-group packed op.  The execution layout is described in eb_internal.h.
+//
+// Arithmetic contracts (elasticbit_runtime.cu line numbers):
+//   decoded weight      w = fp16_rn(f32(q) * s_r)                   (:233-234, :665, :679)
+//   integer-dot output  y = fp16_rn(s_r * sum_c q_rc * x_c)         (:538-558, :594-608)
+//   W16A16 output       y = fp16_rn(sum_c w_rc * x_c)               (:635-647)
+//   bias                y = fp16_rn(y + bias), as torch adds it     (core.py:457-459)
+// All sums accumulate in fp32 on the matrix cores.
+#include "eb_internal.h"
+
+#include <hip/hip_runtime.h>
+
+namespace ebk {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// plane geometry
+// ---------------------------------------------------------------------------
+
+template <int B>
+struct Planes {
+    static_assert(B >= 3 && B <= 15, "compressed widths only");
+    static constexpr bool h8 = (B & 8) != 0;
+    static constexpr bool h4 = (B & 4) != 0;
+    static constexpr bool h2 = (B & 2) != 0;
+    static constexpr bool h1 = (B & 1) != 0;
+    static constexpr int off4 = h8 ? 8 : 0;           // bit offset of each plane in u
+    static constexpr int off2 = off4 + (h4 ? 4 : 0);
+    static constexpr int off1 = off2 + (h2 ? 2 : 0);
+    static constexpr int qmax = (1 << (B - 1)) - 1;
+};
+
+// Raw plane words of one 32-code group.
+template <int B>
+struct Raw {
+    uint32_t d8[8];
+    uint32_t d4[4];
+    uint32_t d2[2];
+    uint32_t d1;
+};
+
+template <int B>
+__device__ __forceinline__ void raw_zero(Raw<B>& r) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r.d8[i] = 0u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.d4[i] = 0u;
+    r.d2[0] = r.d2[1] = 0u;
+    r.d1 = 0u;
+}
+
+template <int B>
+__device__ __forceinline__ void raw_load(const DevMatrix& m, size_t g, Raw<B>& r) {
+    using P = Planes<B>;
+    if constexpr (P::h8) {
+        const uint4* p = reinterpret_cast<const uint4*>(m.p8) + 2 * g;
+        const uint4 a = p[0];
+        const uint4 b = p[1];
+        r.d8[0] = a.x; r.d8[1] = a.y; r.d8[2] = a.z; r.d8[3] = a.w;
+        r.d8[4] = b.x; r.d8[5] = b.y; r.d8[6] = b.z; r.d8[7] = b.w;
+    }
+    if constexpr (P::h4) {
+        const uint4 a = reinterpret_cast<const uint4*>(m.p4)[g];
+        r.d4[0] = a.x; r.d4[1] = a.y; r.d4[2] = a.z; r.d4[3] = a.w;
+    }
+    if constexpr (P::h2) {
+        const uint2 a = reinterpret_cast<const uint2*>(m.p2)[g];
+        r.d2[0] = a.x; r.d2[1] = a.y;
+    }
+    if constexpr (P::h1) {
+        r.d1 = reinterpret_cast<const uint32_t*>(m.p1)[g];
+    }
+}
+
+// Quad d (codes 4d..4d+3) as byte lanes: lo = bits 0..7 of each u, hi = bits 8+.
+template <int B>
+__device__ __forceinline__ void quad_bytes(const Raw<B>& r, int d, uint32_t& lo, uint32_t& hi) {
+    using P = Planes<B>;
+    constexpr int base = P::h8 ? 8 : 0;
+    uint32_t small = 0u;
+    if constexpr (P::h4) small |= ((r.d4[d >> 1] >> (4 * (d & 1))) & 0x0F0F0F0Fu) << (P::off4 - base);
+    if constexpr (P::h2) small |= ((r.d2[d >> 2] >> (2 * (d & 3))) & 0x03030303u) << (P::off2 - base);
+    if constexpr (P::h1) small |= ((r.d1 >> d) & 0x01010101u) << (P::off1 - base);
+    if constexpr (P::h8) {
+        lo = r.d8[d];
+        hi = small;
+    } else {
+        lo = small;
+        hi = 0u;
+    }
+}
+
+__device__ __forceinline__ uint32_t pack_h2(_Float16 a, _Float16 b) {
+    half2v v = {a, b};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+// Exact fp16 codes q for one quad, b <= 10: the byte lanes become the
+// mantissa of 1024 + u (fp16 0x6400 | u), then 1024 + qmax is subtracted.
+template <int B>
+__device__ __forceinline__ void quad_q(uint32_t lo, uint32_t hi, uint32_t& w0, uint32_t& w1) {
+    static_assert(B <= 10, "fp16 mantissa holds at most 10 code bits");
+    const uint32_t H = hi | 0x64646464u;
+    const uint32_t a = __builtin_amdgcn_perm(H, lo, 0x05010400u);  // [lo0 H0 lo1 H1]
+    const uint32_t b = __builtin_amdgcn_perm(H, lo, 0x07030602u);  // [lo2 H2 lo3 H3]
+    constexpr _Float16 off = static_cast<_Float16>(1024 + Planes<B>::qmax);
+    const half2v o = {off, off};
+    w0 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, a) - o);
+    w1 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, b) - o);
+}
+
+// Exact decoded weights fp16_rn(f32(q) * s) for one quad (any b <= 15).
+template <int B>
+__device__ __forceinline__ void quad_w(uint32_t lo, uint32_t hi, float s, uint32_t& w0, uint32_t& w1) {
+    _Float16 h[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int u = static_cast<int>(((lo >> (8 * j)) & 0xFFu) | (((hi >> (8 * j)) & 0xFFu) << 8));
+        const float q = static_cast<float>(u - Planes<B>::qmax);
+        h[j] = static_cast<_Float16>(q * s);
+    }
+    w0 = pack_h2(h[0], h[1]);
+    w1 = pack_h2(h[2], h[3]);
+}
+
+enum Mode { kModeQ = 0, kModeW = 1, kModeRaw = 2 };
+
+// Decode the 8 codes [8t, 8t+8) of a group into an MFMA operand.
+template <int B, int MODE>
+__device__ __forceinline__ half8 decode8(const Raw<B>& r, int t, float s) {
+    uint32_t w[4];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        uint32_t lo, hi;
+        quad_bytes<B>(r, 2 * t + h, lo, hi);
+        if constexpr (MODE == kModeQ) {
+            quad_q<B>(lo, hi, w[2 * h], w[2 * h + 1]);
+        } else {
+            quad_w<B>(lo, hi, s, w[2 * h], w[2 * h + 1]);
+        }
+    }
+    uint4 v = {w[0], w[1], w[2], w[3]};
+    return __builtin_bit_cast(half8, v);
+}
+
+// ---------------------------------------------------------------------------
+// bit-exact canonical extraction (elasticbit_runtime.cu:188-206)
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ uint32_t extract_canon(const uint8_t* p, uint64_t nbytes, uint64_t index, int bits) {
+    const uint64_t bit = index * static_cast<uint64_t>(bits);
+    const uint64_t byte = bit >> 3;
+    uint32_t word = 0u;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        if (byte + k < nbytes) word |= static_cast<uint32_t>(p[byte + k]) << (8 * k);
+    }
+    return (word >> (bit & 7u)) & ((1u << bits) - 1u);
+}
+
+template <int B>
+__global__ void repack_kernel(const uint8_t* __restrict__ canon, uint64_t canon_bytes, DevMatrixOut out,
+                              uint64_t groups) {
+    using P = Planes<B>;
+    const uint64_t g = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (g >= groups) return;
+    const uint64_t row = g / static_cast<uint64_t>(out.gpr);
+    const int col0 = static_cast<int>(g - row * out.gpr) * kGroup;
+    uint32_t d8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    uint32_t d4[4] = {0, 0, 0, 0};
+    uint32_t d2[2] = {0, 0};
+    uint32_t d1 = 0u;
+#pragma unroll 4
+    for (int i = 0; i < kGroup; ++i) {
+        const int col = col0 + i;
+        const uint32_t u = col < out.cols
+            ? extract_canon(canon, canon_bytes, row * static_cast<uint64_t>(out.cols) + col, B)
+            : static_cast<uint32_t>(P::qmax);
+        const int j = i & 3;
+        const int d = i >> 2;
+        if constexpr (P::h8) d8[d] |= (u & 0xFFu) << (8 * j);
+        if constexpr (P::h4) d4[d >> 1] |= ((u >> P::off4) & 0xFu) << (8 * j + 4 * (d & 1));
+        if constexpr (P::h2) d2[d >> 2] |= ((u >> P::off2) & 0x3u) << (8 * j + 2 * (d & 3));
+        if constexpr (P::h1) d1 |= ((u >> P::off1) & 0x1u) << (8 * j + d);
+    }
+    if constexpr (P::h8) {
+        uint4* p = reinterpret_cast<uint4*>(out.p8) + 2 * g;
+        p[0] = make_uint4(d8[0], d8[1], d8[2], d8[3]);
+        p[1] = make_uint4(d8[4], d8[5], d8[6], d8[7]);
+    }
+    if constexpr (P::h4) reinterpret_cast<uint4*>(out.p4)[g] = make_uint4(d4[0], d4[1], d4[2], d4[3]);
+    if constexpr (P::h2) reinterpret_cast<uint2*>(out.p2)[g] = make_uint2(d2[0], d2[1]);
+    if constexpr (P::h1) reinterpret_cast<uint32_t*>(out.p1)[g] = d1;
+}
+
+__global__ void repack16_kernel(const uint16_t* __restrict__ canon, DevMatrixOut out, uint64_t groups) {
+    const uint64_t g = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (g >= groups) return;
+    const uint64_t row = g / static_cast<uint64_t>(out.gpr);
+    const int col0 = static_cast<int>(g - row * out.gpr) * kGroup;
+    uint16_t* dst = out.w16 + g * kGroup;
+    for (int i = 0; i < kGroup; ++i) {
+        const int col = col0 + i;
+        dst[i] = col < out.cols ? canon[row * static_cast<uint64_t>(out.cols) + col] : uint16_t(0);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// unpack / materialize (one thread per group)
+// ---------------------------------------------------------------------------
+
+template <int B>
+__global__ void unpack_kernel(DevMatrix m, int16_t* __restrict__ out, uint64_t groups) {
+    const uint64_t g = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (g >= groups) return;
+    const uint64_t row = g / static_cast<uint64_t>(m.gpr);
+    const int col0 = static_cast<int>(g - row * m.gpr) * kGroup;
+    Raw<B> r;
+    raw_load<B>(m, g, r);
+    int16_t* dst = out + row * static_cast<uint64_t>(m.cols);
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+        uint32_t lo, hi;
+        quad_bytes<B>(r, d, lo, hi);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int col = col0 + 4 * d + j;
+            const int u = static_cast<int>(((lo >> (8 * j)) & 0xFFu) | (((hi >> (8 * j)) & 0xFFu) << 8));
+            if (col < m.cols) dst[col] = static_cast<int16_t>(u - Planes<B>::qmax);
+        }
+    }
+}
+
+template <int B>
+__global__ void materialize_kernel(DevMatrix m, uint16_t* __restrict__ out, uint64_t groups) {
+    const uint64_t g = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (g >= groups) return;
+    const uint64_t row = g / static_cast<uint64_t>(m.gpr);
+    const int col0 = static_cast<int>(g - row * m.gpr) * kGroup;
+    uint16_t* dst = out + row * static_cast<uint64_t>(m.cols);
+    if constexpr (B == 16) {
+        const uint16_t* src = m.w16 + g * kGroup;
+        for (int i = 0; i < kGroup; ++i) {
+            if (col0 + i < m.cols) dst[col0 + i] = src[i];
+        }
+    } else {
+        Raw<B> r;
+        raw_load<B>(m, g, r);
+        const float s = m.scales[row];
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+            uint32_t lo, hi, w0, w1;
+            quad_bytes<B>(r, d, lo, hi);
+            quad_w<B>(lo, hi, s, w0, w1);
+            const uint32_t ws[4] = {w0 & 0xFFFFu, w0 >> 16, w1 & 0xFFFFu, w1 >> 16};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int col = col0 + 4 * d + j;
+                if (col < m.cols) dst[col] = static_cast<uint16_t>(ws[j]);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// shared pieces of the linear kernels
+// ---------------------------------------------------------------------------
+
+// fp16 bits -> float and float -> fp16 bits (round to nearest even).
+__device__ __forceinline__ float h2f(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f)); }
+
+// Output epilogue: integer-dot scale, fp16 rounding, then torch-style bias add.
+template <int MODE>
+__device__ __forceinline__ uint16_t epilogue(float acc, float s, const uint16_t* bias, int n) {
+    uint16_t y = f2h(MODE == kModeQ ? acc * s : acc);
+    if (bias) y = f2h(h2f(y) + h2f(bias[n]));
+    return y;
+}
+
+// Load the 32 activations x[row][k0 .. k0+32) as four 8-half MFMA operands,
+// zero beyond `cols`.  vec: cols % 8 == 0 and x 16-byte aligned.
+__device__ __forceinline__ void load_x32(const uint16_t* __restrict__ xrow, int k0, int cols, bool vec,
+                                         half8 (&a)[4]) {
+    if (vec && k0 + kGroup <= cols) {
+        const uint4* p = reinterpret_cast<const uint4*>(xrow + k0);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) a[t] = __builtin_bit_cast(half8, p[t]);
+    } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int k = k0 + 8 * t + i;
+                a[t][i] = k < cols ? __builtin_bit_cast(_Float16, xrow[k]) : static_cast<_Float16>(0.0f);
+            }
+        }
+    }
+}
+
+// Raw fp16 group (b = 16): 32 halves as four MFMA operands.
+__device__ __forceinline__ void load_w16(const DevMatrix& m, size_t g, half8 (&b)[4]) {
+    const uint4* p = reinterpret_cast<const uint4*>(m.w16 + g * kGroup);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) b[t] = __builtin_bit_cast(half8, p[t]);
+}
+
+// ---------------------------------------------------------------------------
+// decode kernel, M <= 16: one workgroup owns 16 weight rows; its WAVES waves
+// split the row's groups.  Lane l of a wave takes row n0 + l%16 and group
+// 4*it + l/16, so one iteration feeds four v_mfma_f32_16x16x32_f16 with
+// 16 rows x 128 columns.  The K order inside a group is the same for the A
+// (activation) and B (weight) operands, so any order is a valid dot product.
+// ---------------------------------------------------------------------------
+
+template <int B, int MODE, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void linear_skinny_kernel(
+    DevMatrix m, const uint16_t* __restrict__ x, int M, uint16_t* __restrict__ y,
+    const uint16_t* __restrict__ bias, int xvec) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int nl = lane & 15;
+    const int quarter = lane >> 4;
+    const int row = blockIdx.x * 16 + nl;
+    const bool row_ok = row < m.rows;
+    const bool m_ok = nl < M;                        // activation row of the A operand
+    const int iters = (m.gpr + 3) >> 2;
+    float s = 0.0f;
+    if constexpr (MODE == kModeW) s = row_ok ? m.scales[row] : 0.0f;
+    const uint16_t* xrow = x + static_cast<size_t>(m_ok ? nl : 0) * m.cols;
+
+    floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int it = wave; it < iters; it += WAVES) {
+        const int grp = it * 4 + quarter;
+        const bool g_ok = grp < m.gpr;
+        const size_t g = static_cast<size_t>(row) * m.gpr + grp;
+        half8 a[4];
+        if (m_ok && g_ok) {
+            load_x32(xrow, grp * kGroup, m.cols, xvec != 0, a);
+        } else {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) a[t] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+        if constexpr (MODE == kModeRaw) {
+            half8 b[4];
+            if (row_ok && g_ok) {
+                load_w16(m, g, b);
+            } else {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) b[t] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], b[t], acc, 0, 0, 0);
+        } else {
+            Raw<B> r;
+            if (row_ok && g_ok) raw_load<B>(m, g, r); else raw_zero<B>(r);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const half8 b = decode8<B, MODE>(r, t, s);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], b, acc, 0, 0, 0);
+            }
+        }
+    }
+
+    // cross-wave reduction of the 16x16 fp32 tile
+    __shared__ floatx4 red[WAVES][64];
+    red[wave][lane] = acc;
+    __syncthreads();
+    for (int o = threadIdx.x; o < 256; o += 64 * WAVES) {
+        const int src = o & 63;
+        const int e = o >> 6;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) v += red[w][src][e];
+        const int mi = 4 * (src >> 4) + e;           // D[4*(l/16)+e][l%16]
+        const int n = blockIdx.x * 16 + (src & 15);
+        if (mi < M && n < m.rows) {
+            float sn = 1.0f;
+            if constexpr (MODE == kModeQ) sn = m.scales[n];
+            y[static_cast<size_t>(mi) * m.rows + n] = epilogue<MODE>(v, sn, bias, n);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// prefill kernel, M > 16: 128 x 128 output tiles, K steps of 64 (two groups).
+// Four waves in a 2 x 2 grid each own 64 x 64.  Every K step the workgroup
+// stages the activation tile and the decoded fp16 weight tile in LDS (double
+// buffered) and feeds v_mfma_f32_16x16x32_f16.
+// ---------------------------------------------------------------------------
+
+constexpr int kBM = 128;
+constexpr int kBN = 128;
+constexpr int kBK = 64;
+constexpr int kLDK = kBK + 8;  // padded row (halves) to stagger LDS banks
+
+template <int B, int MODE>
+__global__ __launch_bounds__(256) void linear_gemm_kernel(
+    DevMatrix m, const uint16_t* __restrict__ x, int M, uint16_t* __restrict__ y,
+    const uint16_t* __restrict__ bias, int xvec) {
+    __shared__ __attribute__((aligned(16))) _Float16 xs[2][kBM * kLDK];
+    __shared__ __attribute__((aligned(16))) _Float16 ws[2][kBN * kLDK];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave >> 1;
+    const int wn = wave & 1;
+    const int m0 = blockIdx.y * kBM;
+    const int n0 = blockIdx.x * kBN;
+    const int ktiles = (m.gpr + 1) >> 1;
+
+    // activation loader: rows tid/8 + 32j, 8 halves at column 8*(tid%8)
+    const int xr = tid >> 3;
+    const int xc = (tid & 7) * 8;
+    // weight loader: row tid/2, group 2*kt + (tid & 1)
+    const int wr = tid >> 1;
+    const int wh = tid & 1;
+    const int wrow = n0 + wr;
+    const bool wrow_ok = wrow < m.rows;
+    float ws_scale = 0.0f;
+    if constexpr (MODE == kModeW) ws_scale = wrow_ok ? m.scales[wrow] : 0.0f;
+
+    uint4 xreg[4];
+    Raw<(B == 16 ? 8 : B)> wraw;
+    uint4 w16reg[4];
+
+    auto load_tile = [&](int kt) {
+        const int k0 = kt * kBK;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int r = m0 + xr + 32 * j;
+            const int k = k0 + xc;
+            if (r < M && xvec && k + 8 <= m.cols) {
+                xreg[j] = *reinterpret_cast<const uint4*>(x + static_cast<size_t>(r) * m.cols + k);
+            } else {
+                uint32_t v[4] = {0, 0, 0, 0};
+                if (r < M) {
+                    for (int i = 0; i < 8; ++i) {
+                        if (k + i < m.cols) {
+                            v[i >> 1] |= static_cast<uint32_t>(x[static_cast<size_t>(r) * m.cols + k + i]) << (16 * (i & 1));
+                        }
+                    }
+                }
+                xreg[j] = make_uint4(v[0], v[1], v[2], v[3]);
+            }
+        }
+        const int grp = 2 * kt + wh;
+        const bool ok = wrow_ok && grp < m.gpr;
+        const size_t g = static_cast<size_t>(wrow) * m.gpr + grp;
+        if constexpr (MODE == kModeRaw) {
+            if (ok) {
+                const uint4* p = reinterpret_cast<const uint4*>(m.w16 + g * kGroup);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) w16reg[t] = p[t];
+            } else {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) w16reg[t] = make_uint4(0, 0, 0, 0);
+            }
+        } else {
+            if (ok) raw_load<B>(m, g, wraw); else raw_zero<B>(wraw);
+        }
+    };
+
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            *reinterpret_cast<uint4*>(&xs[buf][(xr + 32 * j) * kLDK + xc]) = xreg[j];
+        }
+        _Float16* wdst = &ws[buf][wr * kLDK + wh * kGroup];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            if constexpr (MODE == kModeRaw) {
+                *reinterpret_cast<uint4*>(wdst + 8 * t) = w16reg[t];
+            } else {
+                *reinterpret_cast<half8*>(wdst + 8 * t) = decode8<B, MODE>(wraw, t, ws_scale);
+            }
+        }
+    };
+
+    floatx4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    load_tile(0);
+    store_tile(0);
+    __syncthreads();
+
+    const int fr = lane & 15;          // operand row inside a 16-row block
+    const int fk = (lane >> 4) * 8;    // operand K offset inside a 32-wide step
+    for (int kt = 0; kt < ktiles; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < ktiles) load_tile(kt + 1);
+#pragma unroll
+        for (int kk = 0; kk < kBK; kk += 32) {
+            half8 af[4], bf[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                af[i] = *reinterpret_cast<const half8*>(&xs[buf][(wm * 64 + 16 * i + fr) * kLDK + kk + fk]);
+                bf[i] = *reinterpret_cast<const half8*>(&ws[buf][(wn * 64 + 16 * i + fr) * kLDK + kk + fk]);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < ktiles) store_tile(buf ^ 1);
+        __syncthreads();
+    }
+
+    // epilogue: lane holds D[4*(lane/16)+e][lane%16] of each 16x16 block
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int n = n0 + wn * 64 + 16 * j + (lane & 15);
+        if (n >= m.rows) continue;
+        float sn = 1.0f;
+        if constexpr (MODE == kModeQ) sn = m.scales[n];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = m0 + wm * 64 + 16 * i + 4 * (lane >> 4) + e;
+                if (r < M) y[static_cast<size_t>(r) * m.rows + n] = epilogue<MODE>(acc[i][j][e], sn, bias, n);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// legacy flat-group op (bolt/ops_cuda.cu:2708-2750): one wave per output
+// feature, four activation rows per wave, lanes stride over K.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float load_as_float(const void* p, int dtype, int64_t i) {
+    if (dtype == 0) return static_cast<const float*>(p)[i];
+    const uint16_t h = static_cast<const uint16_t*>(p)[i];
+    if (dtype == 1) return h2f(h);
+    return __builtin_bit_cast(float, static_cast<uint32_t>(h) << 16);
+}
+
+__device__ __forceinline__ void store_from_float(void* p, int dtype, int64_t i, float v) {
+    if (dtype == 0) {
+        static_cast<float*>(p)[i] = v;
+    } else if (dtype == 1) {
+        static_cast<uint16_t*>(p)[i] = f2h(v);
+    } else {
+        // round to nearest even on the upper 16 bits; NaN stays a quiet NaN
+        const uint32_t u = __builtin_bit_cast(uint32_t, v);
+        uint16_t b;
+        if ((u & 0x7FFFFFFFu) > 0x7F800000u) {
+            b = static_cast<uint16_t>((u >> 16) | 0x40u);
+        } else {
+            b = static_cast<uint16_t>((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+        }
+        static_cast<uint16_t*>(p)[i] = b;
+    }
+}
+
+__global__ void packed_linear_kernel(const void* __restrict__ x, int x_dtype, int64_t M,
+                                     const uint8_t* __restrict__ packed, const void* __restrict__ scales,
+                                     int s_dtype, const void* __restrict__ bias, int bits,
+                                     int64_t group_size, int64_t N, int64_t K, void* __restrict__ y) {
+    constexpr int kRows = 4;
+    const int lane = threadIdx.x;
+    const int64_t o = blockIdx.x;
+    const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kRows;
+    const uint32_t mask = (1u << bits) - 1u;
+    const int qmin = -(1 << (bits - 1));
+    float acc[kRows] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int64_t k = lane; k < K; k += 64) {
+        const int64_t wi = o * K + k;
+        const int64_t bit = wi * bits;
+        const int64_t byte = bit >> 3;
+        const int off = static_cast<int>(bit & 7);
+        uint32_t word = packed[byte];
+        if (off + bits > 8) word |= static_cast<uint32_t>(packed[byte + 1]) << 8;
+        const int q = static_cast<int>((word >> off) & mask) + qmin;
+        const float w = static_cast<float>(q) * load_as_float(scales, s_dtype, wi / group_size);
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) {
+            if (m0 + r < M) acc[r] += load_as_float(x, x_dtype, (m0 + r) * K + k) * w;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+        float v = acc[r];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+        acc[r] = v;
+    }
+    if (lane == 0) {
+        const float b = bias ? load_as_float(bias, x_dtype, o) : 0.0f;
+        for (int r = 0; r < kRows; ++r) {
+            if (m0 + r < M) store_from_float(y, x_dtype, (m0 + r) * N + o, acc[r] + b);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// dispatch helpers
+// ---------------------------------------------------------------------------
+
+inline unsigned blocks_for(uint64_t n, unsigned threads) {
+    return static_cast<unsigned>((n + threads - 1) / threads);
+}
+
+template <template <int> class F, typename... Args>
+hipError_t dispatch_bits(int bits, Args&&... args) {
+    switch (bits) {
+        case 3: return F<3>::run(args...);
+        case 4: return F<4>::run(args...);
+        case 5: return F<5>::run(args...);
+        case 6: return F<6>::run(args...);
+        case 7: return F<7>::run(args...);
+        case 8: return F<8>::run(args...);
+        case 9: return F<9>::run(args...);
+        case 10: return F<10>::run(args...);
+        case 11: return F<11>::run(args...);
+        case 12: return F<12>::run(args...);
+        case 13: return F<13>::run(args...);
+        case 14: return F<14>::run(args...);
+        case 15: return F<15>::run(args...);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+template <int B>
+struct RepackOp {
+    static hipError_t run(const uint8_t* canon, uint64_t canon_bytes, const DevMatrixOut& out, hipStream_t s) {
+        const uint64_t groups = static_cast<uint64_t>(out.rows) * out.gpr;
+        hipLaunchKernelGGL(repack_kernel<B>, dim3(blocks_for(groups, 256)), dim3(256), 0, s,
+                           canon, canon_bytes, out, groups);
+        return hipGetLastError();
+    }
+};
+
+template <int B>
+struct UnpackOp {
+    static hipError_t run(const DevMatrix& m, int16_t* out, hipStream_t s) {
+        const uint64_t groups = static_cast<uint64_t>(m.rows) * m.gpr;
+        hipLaunchKernelGGL(unpack_kernel<B>, dim3(blocks_for(groups, 256)), dim3(256), 0, s, m, out, groups);
+        return hipGetLastError();
+    }
+};
+
+template <int B>
+struct MaterializeOp {
+    static hipError_t run(const DevMatrix& m, uint16_t* out, hipStream_t s) {
+        const uint64_t groups = static_cast<uint64_t>(m.rows) * m.gpr;
+        hipLaunchKernelGGL(materialize_kernel<B>, dim3(blocks_for(groups, 256)), dim3(256), 0, s, m, out,
+                           groups);
+        return hipGetLastError();
+    }
+};
+
+constexpr int kSkinnyWaves = 8;
+constexpr int kSkinnyMaxM = 16;
+
+template <int B, int MODE>
+hipError_t run_linear_mode(const DevMatrix& m, const uint16_t* x, int64_t M, uint16_t* y,
+                           const uint16_t* bias, int xvec, hipStream_t s) {
+    if (M <= kSkinnyMaxM) {
+        hipLaunchKernelGGL((linear_skinny_kernel<B, MODE, kSkinnyWaves>), dim3((m.rows + 15) / 16),
+                           dim3(64 * kSkinnyWaves), 0, s, m, x, static_cast<int>(M), y, bias, xvec);
+    } else {
+        const dim3 grid((m.rows + kBN - 1) / kBN, static_cast<unsigned>((M + kBM - 1) / kBM));
+        hipLaunchKernelGGL((linear_gemm_kernel<B, MODE>), grid, dim3(256), 0, s, m, x,
+                           static_cast<int>(M), y, bias, xvec);
+    }
+    return hipGetLastError();
+}
+
+template <int B>
+struct LinearOp {
+    static hipError_t run(const DevMatrix& m, bool exact_w16, const uint16_t* x, int64_t M, uint16_t* y,
+                          const uint16_t* bias, int xvec, hipStream_t s) {
+        if constexpr (B <= 10) {
+            if (!exact_w16) return run_linear_mode<B, kModeQ>(m, x, M, y, bias, xvec, s);
+        }
+        return run_linear_mode<B, kModeW>(m, x, M, y, bias, xvec, s);
+    }
+};
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+
+hipError_t launch_repack(const uint8_t* canon, uint64_t canon_bytes, const DevMatrixOut& out,
+                         hipStream_t stream) {
+    if (out.bits == 16) {
+        const uint64_t groups = static_cast<uint64_t>(out.rows) * out.gpr;
+        hipLaunchKernelGGL(repack16_kernel, dim3(blocks_for(groups, 256)), dim3(256), 0, stream,
+                           reinterpret_cast<const uint16_t*>(canon), out, groups);
+        return hipGetLastError();
+    }
+    return dispatch_bits<RepackOp>(out.bits, canon, canon_bytes, out, stream);
+}
+
+hipError_t launch_unpack(const DevMatrix& m, int16_t* out, hipStream_t stream) {
+    return dispatch_bits<UnpackOp>(m.bits, m, out, stream);
+}
+
+hipError_t launch_materialize(const DevMatrix& m, uint16_t* out, hipStream_t stream) {
+    if (m.bits == 16) return MaterializeOp<16>::run(m, out, stream);
+    return dispatch_bits<MaterializeOp>(m.bits, m, out, stream);
+}
+
+hipError_t launch_linear(const DevMatrix& m, bool exact_w16, const uint16_t* x, int64_t M, uint16_t* y,
+                         const uint16_t* bias, hipStream_t stream) {
+    const int xvec = (m.cols % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0);
+    if (m.bits == 16) return run_linear_mode<8, kModeRaw>(m, x, M, y, bias, xvec, stream);
+    return dispatch_bits<LinearOp>(m.bits, m, exact_w16, x, M, y, bias, xvec, stream);
+}
+
+hipError_t launch_packed_linear(const void* x, int x_dtype, int64_t M, const uint8_t* packed,
+                                const void* scales, int scale_dtype, const void* bias, int bits,
+                                int64_t group_size, int64_t N, int64_t K, void* y, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(N), static_cast<unsigned>((M + 3) / 4));
+    hipLaunchKernelGGL(packed_linear_kernel, grid, dim3(64), 0, stream, x, x_dtype, M, packed, scales,
+                       scale_dtype, bias, bits, group_size, N, K, y);
+    return hipGetLastError();
+}
+
+}  // namespace ebk

@@ -1,0 +1,210 @@
+"""Host side of libelasticbit_hip.so against the oracle (CPU only).
+
+Covers the C ABI's exported symbols, the canonical packer, the MLB4 reader and
+writer, the host analyzer and host dequantize.  No call here touches a GPU:
+without a device the library builds host-only matrices.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+from oracle import oracle as ora
+
+native = pytest.importorskip("mlbricks_amd.elasticbit._native")
+RM = native.RuntimeMatrix
+
+
+def header_symbols() -> set[str]:
+    text = (ROOT / "include" / "elasticbit.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(eb_[a-z0-9_]+)\s*\(", text))
+
+
+def test_library_exports_every_declared_symbol():
+    syms = header_symbols()
+    assert len(syms) >= 20
+    lib = native.lib()
+    for name in sorted(syms):
+        assert hasattr(lib, name), f"{name} declared in include/elasticbit.h but not exported"
+    assert lib.eb_abi_version() == 1
+
+
+def test_backend_info_without_device_is_safe():
+    info = native.backendInfo()
+    assert info["activateDType"] == "float16"
+    assert info["weightWidths"] == tuple(range(3, 17))
+    assert info["prefill"] == "native"
+    if not info["available"]:
+        assert info["deviceIndex"] == -1
+
+
+@pytest.mark.parametrize("b", [3, 4, 5, 7, 8, 9, 10, 11, 15])
+@pytest.mark.parametrize("rows,cols", [(1, 1), (7, 13), (8, 31), (17, 32), (33, 65), (5, 1000)])
+def test_host_pack_matches_oracle(b, rows, cols):
+    qm = (1 << (b - 1)) - 1
+    rng = np.random.default_rng(rows * 31 + cols * 7 + b)
+    codes = rng.integers(-qm, qm + 1, size=(rows, cols)).astype(np.int16)
+    ours = native.host_pack_codes(codes, b)
+    assert np.array_equal(ours, ora.pack_codes(codes, b))
+    assert np.array_equal(native.host_unpack_codes(ours, codes.size, b), codes.reshape(-1))
+
+
+def test_host_pack_rejects_out_of_range():
+    with pytest.raises(ValueError, match="exceeds selected bit range"):
+        native.host_pack_codes(np.array([8], np.int16), 4)
+
+
+@pytest.mark.parametrize("b", range(3, 16))
+def test_compress_selected_codes_canonical_and_dequantize(golden, b):
+    w = golden["w"]
+    q = golden[f"codes_b{b}"]
+    s = golden[f"scales_b{b}"]
+    m = RM._compressSelectedCodes(q, s, b, 0.01, 0.005)
+    scales, payload = m._canonical()
+    assert np.array_equal(scales, s)
+    assert np.array_equal(payload, golden[f"payload_b{b}"])
+    deq = m.dequantize()
+    assert np.array_equal(deq, golden[f"dec16_b{b}"].view(np.float16).astype(np.float32))
+    assert m.storageBits == b
+    assert m.storageBytes == payload.size + 4 * w.shape[0]
+    assert m.originalBytes == 2 * w.size
+
+
+@pytest.mark.parametrize("b", [3, 8, 10, 15, 16])
+def test_compress_selected_weights_matches_oracle(golden, b):
+    w = golden["w"]
+    m = RM._compressSelected(w, b, 0.01, 0.0)
+    scales, payload = m._canonical()
+    if b == 16:
+        assert scales.size == 0
+        assert np.array_equal(payload, golden["payload_b16"])
+    else:
+        assert np.array_equal(scales, golden[f"scales_b{b}"])
+        assert np.array_equal(payload, golden[f"payload_b{b}"])
+
+
+def test_pack_weights_matches_oracle_on_larger_random():
+    rng = np.random.default_rng(11)
+    w = (rng.standard_normal((67, 301)) * 0.03).astype(np.float16).astype(np.float32)
+    w[:, 7] *= 8
+    for b in (5, 9, 12):
+        m = RM._compressSelected(w, b, 0.01, 0.0)
+        s, p = m._canonical()
+        so = ora.row_scales(w, b)
+        assert np.array_equal(s, so)
+        assert np.array_equal(p, ora.pack_weights(w, b, so))
+        _, d16 = ora.dequantize(p, s, *w.shape, b)
+        assert np.array_equal(m.dequantize(), d16.view(np.float16).astype(np.float32))
+
+
+@pytest.mark.parametrize("b", [3, 8, 10, 16])
+def test_mlb4_load_save_roundtrip_matches_golden_bytes(golden_dir, tmp_path, b):
+    src = golden_dir / f"mlb4_b{b}.mlb"
+    m = RM.load(str(src))
+    assert m.storageBits == b
+    assert m.shape == (8, 32)
+    assert m.threshold == 0.01
+    out = tmp_path / "copy.mlb"
+    m.save(str(out))
+    assert out.read_bytes() == src.read_bytes()
+
+
+@pytest.mark.parametrize("b", [3, 8, 10, 16])
+def test_mlb4_corruption_and_truncation_are_rejected(golden_dir, tmp_path, b):
+    with pytest.raises(RuntimeError, match="checksum mismatch"):
+        RM.load(str(golden_dir / f"mlb4_b{b}_corrupt.mlb"))
+    data = (golden_dir / f"mlb4_b{b}.mlb").read_bytes()
+    short = tmp_path / "short.mlb"
+    short.write_bytes(data[:-1])
+    with pytest.raises(RuntimeError, match="invalid ElasticBit MLB4 metadata"):
+        RM.load(str(short))
+    bad = tmp_path / "magic.mlb"
+    bad.write_bytes(b"MLB5" + data[4:])
+    with pytest.raises(RuntimeError, match="invalid ElasticBit MLB4 file"):
+        RM.load(str(bad))
+    with pytest.raises(RuntimeError, match="failed to open"):
+        RM.load(str(tmp_path / "missing.mlb"))
+
+
+def test_analyzer_bit_exact_against_oracle():
+    rng = np.random.default_rng(20260918)
+    w = rng.normal(0, 0.04, size=(96, 128)).astype(np.float32)
+    c = rng.normal(0, 1, size=(12, 128)).astype(np.float32)
+    ours = native.analyze(w, c, 0.02)
+    ref = ora.analyze(w, c)
+    for a, r in zip(ours["candidates"], ref):
+        assert a["bits"] == r["bits"]
+        assert a["hardwareNativeError"] == r["hardwareNativeError"]
+        assert a["fullPrecisionError"] == r["fullPrecisionError"]
+        assert a["storageBytes"] == r["storageBytes"]
+        assert a["passes"] == (r["error"] <= 0.02)
+    assert ours["selectedBits"] == ref[ora.select(ref, 0.02)]["bits"]
+    assert ours["selectedError"] <= 0.02
+
+
+def test_analyzer_matches_pure_python_golden(golden):
+    ours = native.analyze(golden["analyze_w"], golden["analyze_calib"], 0.01)
+    for a, (b, hw, fp) in zip(ours["candidates"], golden["analyze_errors"]):
+        assert a["bits"] == int(b)
+        np.testing.assert_allclose(a["hardwareNativeError"], hw, rtol=1e-12, atol=1e-300)
+        np.testing.assert_allclose(a["fullPrecisionError"], fp, rtol=1e-12, atol=1e-300)
+
+
+def test_compress_uses_analyzer_selection():
+    rng = np.random.default_rng(5)
+    w = rng.normal(0, 0.02, size=(40, 64)).astype(np.float32)
+    c = rng.normal(0, 1, size=(6, 64)).astype(np.float32)
+    a = native.analyze(w, c, 0.01)
+    m = RM.compress(w, c, 0.01)
+    assert m.storageBits == a["selectedBits"]
+    assert m.error == a["selectedError"]
+    s, p = m._canonical()
+    if m.storageBits < 16:
+        assert np.array_equal(p, ora.pack_weights(w, m.storageBits, ora.row_scales(w, m.storageBits)))
+
+
+def test_argument_validation_messages():
+    q = np.zeros((2, 4), np.int16)
+    with pytest.raises(ValueError, match="scales must contain one value per weight row"):
+        RM._compressSelectedCodes(q, np.ones(3, np.float32), 8, 0.01, 0.0)
+    with pytest.raises(ValueError, match="finite and positive"):
+        RM._compressSelectedCodes(q, np.array([1.0, 0.0], np.float32), 8, 0.01, 0.0)
+    with pytest.raises(ValueError, match="between 3 and 16"):
+        RM._compressSelectedCodes(q, np.ones(2, np.float32), 2, 0.01, 0.0)
+    with pytest.raises(ValueError, match="3..15-bit"):
+        RM._compressSelectedCodes(q, np.ones(2, np.float32), 16, 0.01, 0.0)
+    with pytest.raises(ValueError, match="does not satisfy threshold"):
+        RM._compressSelectedCodes(q, np.ones(2, np.float32), 8, 0.01, 0.5)
+    with pytest.raises(ValueError, match="finite non-negative"):
+        native.analyze(np.ones((2, 2)), np.ones((1, 2)), float("nan"))
+    with pytest.raises(ValueError, match="both be 2D"):
+        native.analyze(np.ones(2), np.ones((1, 2)), 0.1)
+    with pytest.raises(ValueError, match="decodePolicy"):
+        RM._compressSelectedCodes(q, np.ones(2, np.float32), 8, 0.01, 0.0, decodePolicy="fast")
+
+
+def test_policy_switch_changes_execution_semantics_metadata():
+    m = RM._compressSelectedCodes(np.zeros((4, 32), np.int16), np.ones(4, np.float32), 10, 0.01, 0.0)
+    assert m.decodePolicy == "hardwareNative"
+    assert m.executionWidth == 10
+    assert m.executionPlanner == "gfx950BitPlane"
+    m.setDecodePolicy("fullPrecision")
+    assert m.decodePolicy == "fullPrecision"
+    assert m.executionWidth == 16
+    assert m.executionPlanner == "fullPrecision"
+
+
+def test_device_calls_fail_loudly_without_device():
+    info = native.backendInfo()
+    if info["available"]:
+        pytest.skip("a HIP device is present")
+    m = RM._compressSelectedCodes(np.zeros((4, 32), np.int16), np.ones(4, np.float32), 10, 0.01, 0.0)
+    with pytest.raises(RuntimeError, match="CUDA runtime"):
+        m.forward(np.zeros(32, np.float32))
+    with pytest.raises(RuntimeError, match="CUDA runtime"):
+        m._materializeTorch()

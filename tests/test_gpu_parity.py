@@ -1,0 +1,273 @@
+"""GPU parity of the HIP path against the CPU oracle (needs an MI355X).
+
+Bars (from the north star): unpacked integer codes and decoded fp16 weights
+bit-exact; layer outputs within max|y - r| / max|r| <= 2e-3 of the oracle's
+fp64-accumulated result of the same semantics (integer-dot for hardwareNative
+b <= 10, decoded-fp16 W16A16 otherwise).  Every call goes through the C ABI.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as ora
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3   # max|y - r| / max|r|, the north star's output tolerance
+
+
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import mlbricks_amd.elasticbit._native as native   # noqa: F401  (fails loudly if unbuilt)
+    return native
+
+
+@pytest.fixture(scope="module")
+def native():
+    return _need_gpu()
+
+
+def _codes(rng, rows, cols, b):
+    qm = (1 << (b - 1)) - 1
+    return rng.integers(-qm, qm + 1, size=(rows, cols)).astype(np.int16)
+
+
+def _x16(rng, M, cols):
+    return torch.from_numpy(rng.standard_normal((M, cols)).astype(np.float16)).cuda()
+
+
+def _rel_max(y: np.ndarray, ref: np.ndarray) -> float:
+    return float(np.abs(y - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def _reference(payload, scales, rows, cols, b, x16_bits, policy="hardwareNative"):
+    if b <= 10 and policy == "hardwareNative":
+        return ora.linear_intdot(payload, scales, rows, cols, b, x16_bits)
+    return ora.linear_w16(payload, scales, rows, cols, b, x16_bits)
+
+
+def test_backend_reports_gfx950(native):
+    info = native.backendInfo()
+    assert info["available"]
+    assert info["architecture"] == "gfx950"
+    assert info["computeUnits"] >= 1
+
+
+@pytest.mark.parametrize("b", range(3, 16))
+@pytest.mark.parametrize("rows,cols", [(1, 1), (7, 13), (8, 31), (17, 32), (33, 65), (64, 4096)])
+def test_unpack_codes_bit_exact(native, b, rows, cols):
+    rng = np.random.default_rng(1000 * b + rows + cols)
+    q = _codes(rng, rows, cols, b)
+    s = rng.uniform(0.002, 0.05, size=rows).astype(np.float32)
+    m = native.RuntimeMatrix._compressSelectedCodes(q, s, b, 0.01, 0.0)
+    got = m._unpackCodesTorch().cpu().numpy()
+    assert np.array_equal(got, q)
+
+
+@pytest.mark.parametrize("b", list(range(3, 16)) + [16])
+@pytest.mark.parametrize("rows,cols", [(1, 1), (7, 13), (33, 65), (128, 1000)])
+def test_materialize_bit_exact(native, b, rows, cols):
+    rng = np.random.default_rng(7 * b + rows)
+    if b == 16:
+        w = (rng.standard_normal((rows, cols)) * 0.05).astype(np.float32)
+        m = native.RuntimeMatrix._compressSelected(w, 16, 0.01, 0.0)
+        ref16 = w.astype(np.float16).view(np.uint16)
+    else:
+        q = _codes(rng, rows, cols, b)
+        # include tiny scales so some decoded weights are fp16 subnormals
+        s = rng.choice([1e-7, 3e-5, 0.01, 0.37], size=rows).astype(np.float32)
+        m = native.RuntimeMatrix._compressSelectedCodes(q, s, b, 0.01, 0.0)
+        _, ref16 = ora.dequantize(ora.pack_codes(q, b), s, rows, cols, b)
+    got = m._materializeTorch().cpu().numpy().view(np.uint16)
+    assert np.array_equal(got, ref16)
+
+
+@pytest.mark.parametrize("b", [3, 4, 5, 7, 8, 9, 10, 11, 12, 13, 15, 16])
+@pytest.mark.parametrize("M", [1, 3, 16, 17, 64, 200])
+@pytest.mark.parametrize("policy", ["hardwareNative", "fullPrecision"])
+def test_forward_matches_oracle(native, b, M, policy):
+    rows, cols = 96, 320
+    rng = np.random.default_rng(b * 100 + M)
+    if b == 16:
+        w = (rng.standard_normal((rows, cols)) * 0.05).astype(np.float32)
+        m = native.RuntimeMatrix._compressSelected(w, 16, 0.01, 0.0, decodePolicy=policy)
+        payload, s = ora.pack_weights(w, 16), None
+    else:
+        q = _codes(rng, rows, cols, b)
+        s = rng.uniform(0.002, 0.05, size=rows).astype(np.float32)
+        m = native.RuntimeMatrix._compressSelectedCodes(q, s, b, 0.01, 0.0, decodePolicy=policy)
+        payload = ora.pack_codes(q, b)
+    x = _x16(rng, M, cols)
+    y = m.forwardTorch(x).float().cpu().numpy()
+    ref = _reference(payload, s, rows, cols, b, x.cpu().numpy().view(np.uint16), policy)
+    assert y.shape == (M, rows)
+    assert _rel_max(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("b", [4, 10, 13])
+@pytest.mark.parametrize("rows,cols", [(1, 1), (7, 13), (8, 31), (17, 32), (33, 65), (5, 1000)])
+@pytest.mark.parametrize("M", [1, 5, 40])
+def test_forward_ragged_shapes(native, b, rows, cols, M):
+    rng = np.random.default_rng(rows * 31 + cols + M + b)
+    q = _codes(rng, rows, cols, b)
+    s = rng.uniform(0.002, 0.05, size=rows).astype(np.float32)
+    m = native.RuntimeMatrix._compressSelectedCodes(q, s, b, 0.01, 0.0)
+    x = _x16(rng, M, cols)
+    y = m.forwardTorch(x).float().cpu().numpy()
+    ref = _reference(ora.pack_codes(q, b), s, rows, cols, b, x.cpu().numpy().view(np.uint16))
+    assert _rel_max(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("M", [1, 24])
+def test_forward_unaligned_activation_pointer(native, M):
+    rows, cols, b = 40, 256, 10
+    rng = np.random.default_rng(M)
+    q = _codes(rng, rows, cols, b)
+    s = rng.uniform(0.002, 0.05, size=rows).astype(np.float32)
+    m = native.RuntimeMatrix._compressSelectedCodes(q, s, b, 0.01, 0.0)
+    buf = torch.empty(M * cols + 1, dtype=torch.float16, device="cuda")
+    x = buf[1:].view(M, cols)                       # 2-byte offset: scalar activation path
+    x.copy_(_x16(rng, M, cols))
+    assert x.data_ptr() % 16 != 0
+    y = m.forwardTorch(x).float().cpu().numpy()
+    ref = _reference(ora.pack_codes(q, b), s, rows, cols, b, x.cpu().numpy().view(np.uint16))
+    assert _rel_max(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("M", [1, 100])
+def test_forward_bias_is_added_like_torch(native, M):
+    rows, cols, b = 50, 128, 8
+    rng = np.random.default_rng(3)
+    q = _codes(rng, rows, cols, b)
+    s = rng.uniform(0.002, 0.05, size=rows).astype(np.float32)
+    m = native.RuntimeMatrix._compressSelectedCodes(q, s, b, 0.01, 0.0)
+    x = _x16(rng, M, cols)
+    bias = torch.from_numpy(rng.standard_normal(rows).astype(np.float16)).cuda()
+    y0 = m.forwardTorch(x)
+    y1 = m.forwardTorch(x, bias=bias)
+    assert torch.equal(y1, y0 + bias)               # fp16_rn(fp16(y) + b), bit for bit
+
+
+def test_outputs_are_deterministic_across_calls(native):
+    rng = np.random.default_rng(9)
+    q = _codes(rng, 256, 1024, 10)
+    s = rng.uniform(0.002, 0.05, size=256).astype(np.float32)
+    m = native.RuntimeMatrix._compressSelectedCodes(q, s, 10, 0.01, 0.0)
+    for M in (1, 300):
+        x = _x16(rng, M, 1024)
+        assert torch.equal(m.forwardTorch(x), m.forwardTorch(x))
+
+
+def _config_matrix(native, rows, cols, b, seed=0, outliers=True):
+    """BASELINE config weights: N(0, 0.02), 1% of input columns x8, fp16; codes by the oracle."""
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(rows, cols, generator=g) * 0.02
+    if outliers:
+        idx = torch.randperm(cols, generator=torch.Generator().manual_seed(3))[: round(0.01 * cols)]
+        w[:, idx] *= 8
+    w = w.half().float().numpy()
+    s = ora.row_scales(w, b)
+    payload = ora.pack_weights(w, b, s)
+    q = ora.unpack_codes(payload, rows, cols, b)
+    m = native.RuntimeMatrix._compressSelectedCodes(q, s, b, 0.01, 0.0)
+    return m, payload, s
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_config2_decode_gemv_4096(native, M):
+    rows = cols = 4096
+    b = 10
+    m, payload, s = _config_matrix(native, rows, cols, b)
+    x = torch.randn(M, cols, generator=torch.Generator().manual_seed(1)).half().cuda()
+    y = m.forwardTorch(x).float().cpu().numpy()
+    sub = 512 if M > 1 else rows                     # the fp64 oracle on a row prefix
+    ref = ora.linear_intdot(payload[: sub * cols * b // 8], s[:sub], sub, cols, b,
+                            x.cpu().numpy().view(np.uint16))
+    assert _rel_max(y[:, :sub], ref) <= TOL
+    # whole output against a torch fp32 product of the decoded weights
+    wd = m._materializeTorch().float()
+    full = (x.float() @ wd.T.contiguous()).cpu().numpy()
+    assert _rel_max(y, full) <= TOL
+
+
+def test_config4_prefill_gemm_14336(native):
+    rows, cols, b, M = 14336, 4096, 10, 2048
+    m, payload, s = _config_matrix(native, rows, cols, b)
+    x = torch.randn(M, cols, generator=torch.Generator().manual_seed(1)).half().cuda()
+    y = m.forwardTorch(x)
+    torch.cuda.synchronize()
+    sub = 16
+    ref = ora.linear_intdot(payload[: sub * cols * b // 8], s[:sub], sub, cols, b,
+                            x[:256].cpu().numpy().view(np.uint16))
+    assert _rel_max(y[:256, :sub].float().cpu().numpy(), ref) <= TOL
+    wd = m._materializeTorch()
+    full = torch.matmul(x.float(), wd.float().T.contiguous())
+    err = float((y.float() - full).abs().max() / full.abs().max())
+    assert err <= TOL
+    assert torch.isfinite(y).all()
+
+
+def test_materialize_config_matches_oracle_bits(native):
+    rows, cols, b = 512, 4096, 10
+    m, payload, s = _config_matrix(native, rows, cols, b)
+    _, ref16 = ora.dequantize(payload, s, rows, cols, b)
+    assert np.array_equal(m._materializeTorch().cpu().numpy().view(np.uint16), ref16)
+    assert np.array_equal(m._unpackCodesTorch().cpu().numpy(), ora.unpack_codes(payload, rows, cols, b))
+
+
+def test_host_forward_and_benchmark_paths(native):
+    rng = np.random.default_rng(4)
+    q = _codes(rng, 64, 96, 6)
+    s = rng.uniform(0.002, 0.05, size=64).astype(np.float32)
+    m = native.RuntimeMatrix._compressSelectedCodes(q, s, 6, 0.01, 0.0)
+    x = rng.standard_normal(96).astype(np.float32)
+    y = m.forward(x)
+    x16 = x.astype(np.float16)
+    ref = ora.linear_intdot(ora.pack_codes(q, 6), s, 64, 96, 6, x16.view(np.uint16))[0]
+    assert _rel_max(y, ref) <= TOL
+    assert m.benchmark(x, iterations=10) > 0.0
+
+
+@pytest.mark.parametrize("b", [2, 4, 8])
+@pytest.mark.parametrize("g", [13, 32, 7])
+def test_legacy_packed_linear_golden(native, golden, b, g):
+    from mlbricks_amd.native import elastic_linear_packed
+
+    x = torch.from_numpy(golden["legacy_x"]).cuda()
+    packed = torch.from_numpy(golden[f"legacy_packed_b{b}"]).cuda()
+    scales = torch.from_numpy(golden[f"legacy_scales_b{b}_g{g}"]).cuda()
+    bias = torch.from_numpy(golden[f"legacy_bias_b{b}_g{g}"]).cuda()
+    y = elastic_linear_packed(x, packed, scales, bias, b, g, 5, 13).cpu().numpy()
+    np.testing.assert_allclose(y, golden[f"legacy_y_b{b}_g{g}"], rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_legacy_packed_linear_dtypes_and_torch_op(native, dtype):
+    import mlbricks_amd.custom_ops  # noqa: F401  registers torch.ops.mlbricks_native
+    from mlbricks_amd.native import elastic_linear_packed
+
+    rng = np.random.default_rng(2)
+    N, K, b, G = 37, 150, 5, 64
+    u = rng.integers(0, 1 << b, size=N * K)
+    total = 0
+    for i, v in enumerate(u.tolist()):
+        total |= v << (i * b)
+    packed_np = np.frombuffer(total.to_bytes((N * K * b + 7) // 8, "little"), np.uint8).copy()
+    scales_np = rng.uniform(0.01, 0.1, size=(N * K + G - 1) // G).astype(np.float32)
+    x_np = rng.standard_normal((2, 3, K)).astype(np.float32)
+    bias_np = rng.standard_normal(N).astype(np.float32)
+    x = torch.from_numpy(x_np).to("cuda", dtype)
+    scales = torch.from_numpy(scales_np).to("cuda", dtype)
+    bias = torch.from_numpy(bias_np).to("cuda", dtype)
+    packed = torch.from_numpy(packed_np).cuda()
+    y = elastic_linear_packed(x, packed, scales, bias, b, G, N, K)
+    y_op = torch.ops.mlbricks_native.elastic_linear_packed(x, packed, scales, bias, b, G, N, K)
+    assert y.shape == (2, 3, N) and y.dtype == dtype
+    assert torch.equal(y, y_op)
+    ref = ora.packed_linear(x.double().cpu().numpy(), packed_np, scales.double().cpu().numpy(),
+                            bias.double().cpu().numpy(), b, G, N, K).reshape(2, 3, N)
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert _rel_max(y.double().cpu().numpy(), ref) <= tol
