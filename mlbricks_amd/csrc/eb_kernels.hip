@@ -115,6 +115,17 @@ __device__ __forceinline__ void quad_q(uint32_t lo, uint32_t hi, uint32_t& w0, u
     w1 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, b) - o);
 }
 
+// a * b rounded to fp32.  The reference rounds products to fp32 before the
+// fp16 rounding (__float2half_rn(q * s)); left alone the compiler fuses
+// fmul + fptrunc into one v_fma_mix with a single rounding, which differs on
+// rare double-rounding ties.  The empty asm hides the product from that
+// combine and emits no instruction.
+__device__ __forceinline__ float mul_f32(float a, float b) {
+    float p = a * b;
+    __asm__("" : "+v"(p));
+    return p;
+}
+
 // Exact decoded weights fp16_rn(f32(q) * s) for one quad (any b <= 15).
 template <int B>
 __device__ __forceinline__ void quad_w(uint32_t lo, uint32_t hi, float s, uint32_t& w0, uint32_t& w1) {
@@ -123,7 +134,7 @@ __device__ __forceinline__ void quad_w(uint32_t lo, uint32_t hi, float s, uint32
     for (int j = 0; j < 4; ++j) {
         const int u = static_cast<int>(((lo >> (8 * j)) & 0xFFu) | (((hi >> (8 * j)) & 0xFFu) << 8));
         const float q = static_cast<float>(u - Planes<B>::qmax);
-        h[j] = static_cast<_Float16>(q * s);
+        h[j] = static_cast<_Float16>(mul_f32(q, s));
     }
     w0 = pack_h2(h[0], h[1]);
     w1 = pack_h2(h[2], h[3]);
@@ -279,7 +290,7 @@ __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uin
 // Output epilogue: integer-dot scale, fp16 rounding, then torch-style bias add.
 template <int MODE>
 __device__ __forceinline__ uint16_t epilogue(float acc, float s, const uint16_t* bias, int n) {
-    uint16_t y = f2h(MODE == kModeQ ? acc * s : acc);
+    uint16_t y = f2h(MODE == kModeQ ? mul_f32(acc, s) : acc);
     if (bias) y = f2h(h2f(y) + h2f(bias[n]));
     return y;
 }

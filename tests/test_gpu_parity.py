@@ -107,6 +107,31 @@ def test_forward_matches_oracle(native, b, M, policy):
     assert _rel_max(y, ref) <= TOL
 
 
+@pytest.mark.parametrize("b", [4, 9, 10, 11, 12, 15, 16])
+@pytest.mark.parametrize("M", [16, 96])
+@pytest.mark.parametrize("policy", ["hardwareNative", "fullPrecision"])
+def test_one_hot_activations_reproduce_decoded_weights(native, b, M, policy):
+    """With x[m] = e_{k_m} every output is one product w[n][k_m] * 1, so the
+    linear kernels' in-register decode must equal fp16_rn(q*s) bit for bit
+    (decode path M <= 16 and prefill path M > 16, both arithmetic modes)."""
+    rows, cols = 48, 160
+    rng = np.random.default_rng(b + M)
+    if b == 16:
+        w = (rng.standard_normal((rows, cols)) * 0.05).astype(np.float32)
+        m = native.RuntimeMatrix._compressSelected(w, 16, 0.01, 0.0, decodePolicy=policy)
+        dec16 = w.astype(np.float16).view(np.uint16)
+    else:
+        q = _codes(rng, rows, cols, b)
+        s = rng.choice([1e-7, 3e-5, 0.01, 0.37], size=rows).astype(np.float32)
+        m = native.RuntimeMatrix._compressSelectedCodes(q, s, b, 0.01, 0.0, decodePolicy=policy)
+        _, dec16 = ora.dequantize(ora.pack_codes(q, b), s, rows, cols, b)
+    ks = rng.permutation(cols)[:M] if M <= cols else rng.integers(0, cols, size=M)
+    x = torch.zeros(M, cols, dtype=torch.float16, device="cuda")
+    x[torch.arange(M), torch.from_numpy(ks).cuda()] = 1.0
+    y = m.forwardTorch(x).cpu().numpy().view(np.uint16)
+    assert np.array_equal(y, dec16[:, ks].T)
+
+
 @pytest.mark.parametrize("b", [4, 10, 13])
 @pytest.mark.parametrize("rows,cols", [(1, 1), (7, 13), (8, 31), (17, 32), (33, 65), (5, 1000)])
 @pytest.mark.parametrize("M", [1, 5, 40])
