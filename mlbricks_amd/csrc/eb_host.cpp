@@ -510,7 +510,9 @@ struct eb_matrix {
         if (!device_present()) return;
         EB_HIP(hipGetDevice(&device));
         const int gpr = (cols + ebk::kGroup - 1) / ebk::kGroup;
-        const size_t groups = static_cast<size_t>(rows) * gpr;
+        const int spr = (gpr + ebk::kTileGroups - 1) / ebk::kTileGroups;
+        const int rtiles = (rows + ebk::kTileRows - 1) / ebk::kTileRows;
+        const size_t groups = static_cast<size_t>(rtiles) * spr * ebk::kTileSlots;
         size_t offs[6] = {0, 0, 0, 0, 0, 0};
         const int widths[5] = {8, 4, 2, 1, 16};
         size_t total = 0;
@@ -528,6 +530,8 @@ struct eb_matrix {
         out.rows = rows;
         out.cols = cols;
         out.gpr = gpr;
+        out.spr = spr;
+        out.rtiles = rtiles;
         out.bits = bits;
         auto at = [&](int i, int width) -> uint8_t* {
             return ebk::plane_bytes(bits, width, groups) ? base + offs[i] : nullptr;
@@ -547,6 +551,8 @@ struct eb_matrix {
         dev.rows = rows;
         dev.cols = cols;
         dev.gpr = gpr;
+        dev.spr = spr;
+        dev.rtiles = rtiles;
         dev.bits = bits;
         if (bits != kFallbackBits) {
             float* d_scales = reinterpret_cast<float*>(base + offs[5]);

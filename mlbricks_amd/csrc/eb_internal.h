@@ -1,15 +1,21 @@
 // Internal interface between the host runtime (eb_host.cpp) and the gfx950
 // kernels (eb_kernels.hip).  Not installed; the public ABI is include/elasticbit.h.
 //
-// Device execution layout ("bit planes")
-// --------------------------------------
+// Device execution layout ("bit planes" in lane-ordered tiles)
+// -------------------------------------------------------------
 // Canonical ElasticBit storage is one dense LSB-first bitstream of b-bit codes
 // u = q + qmax over the row-major weight index (elasticbit_runtime.cu:150-186).
 // At load time the device re-lays it out, still at b bits per weight, as:
 //
-//  * rows padded to a multiple of 32 columns with u = qmax (q = 0);
-//  * groups of 32 consecutive codes of one row, gpr = ceil(cols/32) per row,
-//    flat group index g = row * gpr + col / 32;
+//  * groups of 32 consecutive codes of one row, gpr = ceil(cols/32) per row;
+//  * tiles of 16 rows x 4 groups (16 x 128 codes).  The matrix is padded to
+//    whole tiles with u = qmax (q = 0): rtiles = ceil(rows/16) row tiles,
+//    spr = ceil(gpr/4) tiles per row tile.  Tile (rt, st) is stored at tile
+//    index rt * spr + st, so a row tile's tiles are contiguous along K;
+//  * inside a tile the 64 groups sit in MFMA lane order, slot l = 16*q + n
+//    for the group q (0..3) of row n (0..15): the slot a wave64 lane loads
+//    for the B operand of v_mfma_f32_16x16x32_f16.  A wave reading one tile
+//    therefore reads one contiguous block (2 KB of the 8-bit plane);
 //  * one array per binary digit of b, "planes" of width 8, 4, 2 and 1 bits.
 //    The widest plane holds the lowest bits of u, the next plane the next
 //    bits, and so on (b = 10: plane8 = u & 0xff, plane2 = u >> 8).  A plane of
@@ -18,7 +24,7 @@
 //    byte i % 4, bit field (i / 4) % (8/w).  Every plane therefore yields the
 //    four codes 4d..4d+3 of a "quad" with one shift and one byte-lane mask,
 //    already aligned to the byte lanes a v_perm_b32 consumes.
-//  * b = 16 keeps raw fp16 weights in the same padded group order.
+//  * b = 16 keeps raw fp16 weights (64 bytes per group) in the same slots.
 //
 // All planes are separate arrays, so each lane's share is a naturally aligned
 // 32/16/8/4-byte chunk and a wave reads every plane fully coalesced.
@@ -31,7 +37,15 @@
 
 namespace ebk {
 
-constexpr int kGroup = 32;
+constexpr int kGroup = 32;      // codes per group
+constexpr int kTileRows = 16;   // rows per tile
+constexpr int kTileGroups = 4;  // groups per tile along a row
+constexpr int kTileSlots = kTileRows * kTileGroups;
+
+// Slot (flat group index in the planes) of group `grp` of row `row`.
+__host__ __device__ inline size_t group_slot(int row, int grp, int spr) {
+    return (static_cast<size_t>(row >> 4) * spr + (grp >> 2)) * kTileSlots + (grp & 3) * kTileRows + (row & 15);
+}
 
 struct DevMatrix {
     const uint8_t* p8 = nullptr;    // [G][32] bytes
@@ -43,6 +57,8 @@ struct DevMatrix {
     int rows = 0;
     int cols = 0;
     int gpr = 0;                    // groups per row
+    int spr = 0;                    // tiles per row tile, ceil(gpr / 4)
+    int rtiles = 0;                 // row tiles, ceil(rows / 16)
     int bits = 0;
 };
 
@@ -55,11 +71,13 @@ struct DevMatrixOut {
     int rows = 0;
     int cols = 0;
     int gpr = 0;
+    int spr = 0;
+    int rtiles = 0;
     int bits = 0;
 };
 
 // Bytes of the plane of width `width` (8, 4, 2, 1; 16 = raw fp16) for
-// `groups` groups; 0 when b has no such plane.
+// `groups` slots (rtiles * spr * 64); 0 when b has no such plane.
 inline size_t plane_bytes(int bits, int width, size_t groups) {
     if (bits == 16) return width == 16 ? groups * 64u : 0u;
     if (width == 16 || (bits & width) == 0) return 0u;
@@ -70,10 +88,10 @@ inline size_t plane_bytes(int bits, int width, size_t groups) {
 hipError_t launch_repack(const uint8_t* canon, uint64_t canon_bytes, const DevMatrixOut& out,
                          hipStream_t stream);
 
-// Planes -> int16 codes q = u - qmax, [rows][cols].
+// Planes -> int16 codes q = u - qmax, [rows][cols] row-major.
 hipError_t launch_unpack(const DevMatrix& m, int16_t* out, hipStream_t stream);
 
-// Planes -> fp16 fp16_rn(q * s), [rows][cols].
+// Planes -> fp16 fp16_rn(q * s), [rows][cols] row-major.
 hipError_t launch_materialize(const DevMatrix& m, uint16_t* out, hipStream_t stream);
 
 // y[M][rows] = x[M][cols] . W^T (+ bias).  exact_w16 selects the decoded-fp16

@@ -175,14 +175,28 @@ __device__ __forceinline__ uint32_t extract_canon(const uint8_t* p, uint64_t nby
     return (word >> (bit & 7u)) & ((1u << bits) - 1u);
 }
 
+// Row and group of slot `slot` of the tiled layout (inverse of group_slot).
+__device__ __forceinline__ void slot_coords(uint64_t slot, int spr, int& row, int& grp) {
+    const uint64_t tile = slot / kTileSlots;
+    const int l = static_cast<int>(slot % kTileSlots);
+    const int rt = static_cast<int>(tile / static_cast<uint64_t>(spr));
+    const int st = static_cast<int>(tile - static_cast<uint64_t>(rt) * spr);
+    row = rt * kTileRows + (l & (kTileRows - 1));
+    grp = st * kTileGroups + l / kTileRows;
+}
+
+// One thread per slot: gathers the slot's 32 codes from the canonical stream
+// (padding rows / columns get u = qmax, i.e. q = 0) and writes every plane.
 template <int B>
 __global__ void repack_kernel(const uint8_t* __restrict__ canon, uint64_t canon_bytes, DevMatrixOut out,
-                              uint64_t groups) {
+                              uint64_t slots) {
     using P = Planes<B>;
     const uint64_t g = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (g >= groups) return;
-    const uint64_t row = g / static_cast<uint64_t>(out.gpr);
-    const int col0 = static_cast<int>(g - row * out.gpr) * kGroup;
+    if (g >= slots) return;
+    int row, grp;
+    slot_coords(g, out.spr, row, grp);
+    const int col0 = grp * kGroup;
+    const bool row_ok = row < out.rows;
     uint32_t d8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     uint32_t d4[4] = {0, 0, 0, 0};
     uint32_t d2[2] = {0, 0};
@@ -190,8 +204,8 @@ __global__ void repack_kernel(const uint8_t* __restrict__ canon, uint64_t canon_
 #pragma unroll 4
     for (int i = 0; i < kGroup; ++i) {
         const int col = col0 + i;
-        const uint32_t u = col < out.cols
-            ? extract_canon(canon, canon_bytes, row * static_cast<uint64_t>(out.cols) + col, B)
+        const uint32_t u = row_ok && col < out.cols
+            ? extract_canon(canon, canon_bytes, static_cast<uint64_t>(row) * out.cols + col, B)
             : static_cast<uint32_t>(P::qmax);
         const int j = i & 3;
         const int d = i >> 2;
@@ -210,15 +224,17 @@ __global__ void repack_kernel(const uint8_t* __restrict__ canon, uint64_t canon_
     if constexpr (P::h1) reinterpret_cast<uint32_t*>(out.p1)[g] = d1;
 }
 
-__global__ void repack16_kernel(const uint16_t* __restrict__ canon, DevMatrixOut out, uint64_t groups) {
+__global__ void repack16_kernel(const uint16_t* __restrict__ canon, DevMatrixOut out, uint64_t slots) {
     const uint64_t g = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (g >= groups) return;
-    const uint64_t row = g / static_cast<uint64_t>(out.gpr);
-    const int col0 = static_cast<int>(g - row * out.gpr) * kGroup;
+    if (g >= slots) return;
+    int row, grp;
+    slot_coords(g, out.spr, row, grp);
+    const int col0 = grp * kGroup;
+    const bool row_ok = row < out.rows;
     uint16_t* dst = out.w16 + g * kGroup;
     for (int i = 0; i < kGroup; ++i) {
         const int col = col0 + i;
-        dst[i] = col < out.cols ? canon[row * static_cast<uint64_t>(out.cols) + col] : uint16_t(0);
+        dst[i] = row_ok && col < out.cols ? canon[static_cast<uint64_t>(row) * out.cols + col] : uint16_t(0);
     }
 }
 
@@ -227,14 +243,16 @@ __global__ void repack16_kernel(const uint16_t* __restrict__ canon, DevMatrixOut
 // ---------------------------------------------------------------------------
 
 template <int B>
-__global__ void unpack_kernel(DevMatrix m, int16_t* __restrict__ out, uint64_t groups) {
+__global__ void unpack_kernel(DevMatrix m, int16_t* __restrict__ out, uint64_t slots) {
     const uint64_t g = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (g >= groups) return;
-    const uint64_t row = g / static_cast<uint64_t>(m.gpr);
-    const int col0 = static_cast<int>(g - row * m.gpr) * kGroup;
+    if (g >= slots) return;
+    int row, grp;
+    slot_coords(g, m.spr, row, grp);
+    const int col0 = grp * kGroup;
+    if (row >= m.rows || col0 >= m.cols) return;
     Raw<B> r;
     raw_load<B>(m, g, r);
-    int16_t* dst = out + row * static_cast<uint64_t>(m.cols);
+    int16_t* dst = out + static_cast<uint64_t>(row) * m.cols;
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
         uint32_t lo, hi;
@@ -249,12 +267,14 @@ __global__ void unpack_kernel(DevMatrix m, int16_t* __restrict__ out, uint64_t g
 }
 
 template <int B>
-__global__ void materialize_kernel(DevMatrix m, uint16_t* __restrict__ out, uint64_t groups) {
+__global__ void materialize_kernel(DevMatrix m, uint16_t* __restrict__ out, uint64_t slots) {
     const uint64_t g = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (g >= groups) return;
-    const uint64_t row = g / static_cast<uint64_t>(m.gpr);
-    const int col0 = static_cast<int>(g - row * m.gpr) * kGroup;
-    uint16_t* dst = out + row * static_cast<uint64_t>(m.cols);
+    if (g >= slots) return;
+    int row, grp;
+    slot_coords(g, m.spr, row, grp);
+    const int col0 = grp * kGroup;
+    if (row >= m.rows || col0 >= m.cols) return;
+    uint16_t* dst = out + static_cast<uint64_t>(row) * m.cols;
     if constexpr (B == 16) {
         const uint16_t* src = m.w16 + g * kGroup;
         for (int i = 0; i < kGroup; ++i) {
@@ -289,9 +309,9 @@ __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uin
 
 // Output epilogue: integer-dot scale, fp16 rounding, then torch-style bias add.
 template <int MODE>
-__device__ __forceinline__ uint16_t epilogue(float acc, float s, const uint16_t* bias, int n) {
+__device__ __forceinline__ uint16_t epilogue(float acc, float s, bool has_bias, uint16_t bias_bits) {
     uint16_t y = f2h(MODE == kModeQ ? mul_f32(acc, s) : acc);
-    if (bias) y = f2h(h2f(y) + h2f(bias[n]));
+    if (has_bias) y = f2h(h2f(y) + h2f(bias_bits));
     return y;
 }
 
@@ -315,86 +335,224 @@ __device__ __forceinline__ void load_x32(const uint16_t* __restrict__ xrow, int 
     }
 }
 
-// Raw fp16 group (b = 16): 32 halves as four MFMA operands.
-__device__ __forceinline__ void load_w16(const DevMatrix& m, size_t g, half8 (&b)[4]) {
-    const uint4* p = reinterpret_cast<const uint4*>(m.w16 + g * kGroup);
+// ---------------------------------------------------------------------------
+// decode kernel, M <= 16: one workgroup owns one row tile (16 weight rows);
+// its WAVES waves split the row tile's K tiles.  In step `st` lane l loads
+// slot l of tile (row tile, st) -- group 4*st + l/16 of row l%16 -- so a
+// wave's load is one contiguous block and one step feeds four
+// v_mfma_f32_16x16x32_f16 with 16 rows x 128 columns.  The K order inside a
+// group is the same for the A (activation) and B (weight) operands, so any
+// order is a valid dot product.
+//
+// At M <= 16 the kernel is bound by HBM latency as much as by bandwidth: a
+// CU's share of a 4096 x 4096 b=10 matrix is ~80 KB, about what it must keep
+// in flight to cover the loaded DRAM latency.  Each wave therefore issues the
+// loads of GPL steps at once and, while it decodes and multiplies one batch,
+// already has the next batch's loads in flight.  Vector loads retire in
+// issue order, so every activation load is issued before the weight loads
+// it must not wait behind.
+//
+// XLDS: the activations (M x K, zero-padded to whole tiles) are staged once
+// per workgroup in LDS, when they fit in kXLdsBytes; otherwise each lane with
+// an activation row loads its A operand from global memory per step.
+// ---------------------------------------------------------------------------
+
+constexpr int kXLdsBytes = 32768;
+
+// One group's weight bits as held in registers between load and decode.
+template <int B, int MODE>
+struct GroupBits {
+    Raw<B> r;
+    __device__ __forceinline__ void load(const DevMatrix& m, size_t g) { raw_load<B>(m, g, r); }
+    __device__ __forceinline__ half8 operand(int t, float s) const { return decode8<B, MODE>(r, t, s); }
+};
+
+template <int B>
+struct GroupBits<B, kModeRaw> {
+    uint4 w[4];
+    __device__ __forceinline__ void load(const DevMatrix& m, size_t g) {
+        const uint4* p = reinterpret_cast<const uint4*>(m.w16 + g * kGroup);
 #pragma unroll
-    for (int t = 0; t < 4; ++t) b[t] = __builtin_bit_cast(half8, p[t]);
+        for (int t = 0; t < 4; ++t) w[t] = p[t];
+    }
+    __device__ __forceinline__ half8 operand(int t, float) const { return __builtin_bit_cast(half8, w[t]); }
+};
+
+// Eight activations x[r][k .. k+8) as one uint4, zero at and beyond `cols`.
+__device__ __forceinline__ uint4 load_x8(const uint16_t* __restrict__ x, int r, int k, int cols, bool vec) {
+    const uint16_t* p = x + static_cast<size_t>(r) * cols + k;
+    if (vec && k + 8 <= cols) return *reinterpret_cast<const uint4*>(p);
+    uint32_t v[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        if (k + i < cols) v[i >> 1] |= static_cast<uint32_t>(p[i]) << (16 * (i & 1));
+    }
+    return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
-// ---------------------------------------------------------------------------
-// decode kernel, M <= 16: one workgroup owns 16 weight rows; its WAVES waves
-// split the row's groups.  Lane l of a wave takes row n0 + l%16 and group
-// 4*it + l/16, so one iteration feeds four v_mfma_f32_16x16x32_f16 with
-// 16 rows x 128 columns.  The K order inside a group is the same for the A
-// (activation) and B (weight) operands, so any order is a valid dot product.
-// ---------------------------------------------------------------------------
+// Load tiles first .. first+GPL-1 of this lane's row tile (clamped to the
+// last tile) into `bits`.
+template <int GPL, typename Bits>
+__device__ __forceinline__ void decode_load_batch(const DevMatrix& m, Bits (&bits)[GPL], size_t slot0, int first,
+                                                  int steps) {
+#pragma unroll
+    for (int j = 0; j < GPL; ++j) {
+        bits[j].load(m, slot0 + static_cast<size_t>(min(first + j, steps - 1)) * kTileSlots);
+    }
+}
 
-template <int B, int MODE, int WAVES>
-__global__ __launch_bounds__(64 * WAVES) void linear_skinny_kernel(
+// Activation operands of one workgroup batch (steps base + wave*GPL + j):
+// from the LDS copy, or from global memory, zero past the last step.
+template <int GPL, bool XLDS>
+__device__ __forceinline__ void decode_activations(half8 (&a)[GPL][4], const DevMatrix& m, int base, int wave,
+                                                   int quarter, bool m_ok, int steps,
+                                                   const uint16_t* __restrict__ xrow, const uint16_t* xsrow,
+                                                   int xvec) {
+    const int first = base + wave * GPL;
+#pragma unroll
+    for (int j = 0; j < GPL; ++j) {
+        const int k0 = ((first + j) * kTileGroups + quarter) * kGroup;
+        const bool ok = m_ok && first + j < steps;
+        if constexpr (XLDS) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                a[j][t] = ok ? *reinterpret_cast<const half8*>(xsrow + k0 + 8 * t) : half8{0, 0, 0, 0, 0, 0, 0, 0};
+            }
+        } else if (ok) {
+            load_x32(xrow, k0, m.cols, xvec != 0, a[j]);
+        } else {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) a[j][t] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+    }
+}
+
+// Decode the batch held in `cur` and accumulate it against `a`.
+template <int B, int MODE, int GPL, typename Bits>
+__device__ __forceinline__ void decode_mul_batch(const Bits (&cur)[GPL], const half8 (&a)[GPL][4], int first,
+                                                 int steps, float s, floatx4& acc) {
+#pragma unroll
+    for (int j = 0; j < GPL; ++j) {
+        const bool st_ok = first + j < steps;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            half8 b = cur[j].operand(t, s);
+            if constexpr (MODE == kModeRaw) {
+                if (!st_ok) b = half8{0, 0, 0, 0, 0, 0, 0, 0};
+            }
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j][t], b, acc, 0, 0, 0);
+        }
+    }
+}
+
+template <int B, int MODE, int WAVES, int GPL, bool XLDS>
+__global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
     DevMatrix m, const uint16_t* __restrict__ x, int M, uint16_t* __restrict__ y,
     const uint16_t* __restrict__ bias, int xvec) {
+    using Bits = GroupBits<B, MODE>;
+    constexpr int kThreads = 64 * WAVES;
+    constexpr int kBatch = WAVES * GPL;              // steps per workgroup batch
+    constexpr int kXVecs = kXLdsBytes / 16 / kThreads;
+    static_assert(kXVecs >= 1, "LDS activation staging needs one uint4 per thread");
+    static_assert(kThreads >= 256, "the epilogue stores the 16x16 tile with one thread per element");
+    extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   // [M][spr * 128], XLDS only
+
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int nl = lane & 15;
     const int quarter = lane >> 4;
-    const int row = blockIdx.x * 16 + nl;
-    const bool row_ok = row < m.rows;
+    const int row = blockIdx.x * kTileRows + nl;
     const bool m_ok = nl < M;                        // activation row of the A operand
-    const int iters = (m.gpr + 3) >> 2;
+    const int steps = m.spr;
+    const int kpad = steps * kTileGroups * kGroup;
     float s = 0.0f;
-    if constexpr (MODE == kModeW) s = row_ok ? m.scales[row] : 0.0f;
-    const uint16_t* xrow = x + static_cast<size_t>(m_ok ? nl : 0) * m.cols;
+    if constexpr (MODE == kModeW) s = row < m.rows ? m.scales[row] : 0.0f;
+    // Thread o < 256 stores output (4*(o%64/16) + o/64, n0 + o%16) at the end;
+    // its row scale and bias are loaded now, ahead of the weights, so that
+    // the epilogue does not wait for another memory round trip.
+    const int on = blockIdx.x * kTileRows + (threadIdx.x & 15);
+    float out_scale = 1.0f;
+    uint16_t out_bias = 0;
+    if (threadIdx.x < 256 && on < m.rows) {
+        if constexpr (MODE == kModeQ) out_scale = m.scales[on];
+        if (bias) out_bias = bias[on];
+    }
+    // Slot of this lane in the row tile's first tile; step st adds st * 64.
+    const size_t slot0 = static_cast<size_t>(blockIdx.x) * steps * kTileSlots + lane;
 
+    uint4 xv[XLDS ? kXVecs : 1];
+    const int vpr = kpad / 8;                        // uint4 vectors per staged row
+    if constexpr (XLDS) {
+#pragma unroll
+        for (int r = 0; r < kXVecs; ++r) {
+            const int i = threadIdx.x + r * kThreads;
+            xv[r] = make_uint4(0, 0, 0, 0);
+            if (i < M * vpr) {
+                const int mi = i / vpr;
+                xv[r] = load_x8(x, mi, (i - mi * vpr) * 8, m.cols, xvec != 0);
+            }
+        }
+    }
+
+    // Steps past the end (steps % kBatch != 0) reload the last tile; they
+    // meet zero activations, and raw fp16 weights, which could hold Inf or
+    // NaN, are zeroed there.
     floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int it = wave; it < iters; it += WAVES) {
-        const int grp = it * 4 + quarter;
-        const bool g_ok = grp < m.gpr;
-        const size_t g = static_cast<size_t>(row) * m.gpr + grp;
-        half8 a[4];
-        if (m_ok && g_ok) {
-            load_x32(xrow, grp * kGroup, m.cols, xvec != 0, a);
-        } else {
+    Bits buf0[GPL], buf1[GPL];
+    const int nb = (steps + kBatch - 1) / kBatch;    // workgroup batches
+    const uint16_t* xrow = x + static_cast<size_t>(m_ok ? nl : 0) * m.cols;
+    const uint16_t* xsrow = xs + static_cast<size_t>(m_ok ? nl : 0) * kpad;
+    half8 a[GPL][4];
+
+    // One batch is prefetched while the previous one is multiplied (two
+    // register buffers alternate, so no register copy waits on loads in
+    // flight; every branch is uniform).  The activations of a batch are read
+    // before the next batch's weights are issued, so that waiting for them
+    // (global loads when they are not staged in LDS) does not wait for those
+    // weights.  Keeping more batches in flight per wave measured slower on
+    // MI355X: one tile per wave plus the prefetch keeps ~40 KB per CU in
+    // flight, which already covers the loaded HBM latency.
+    decode_load_batch<GPL>(m, buf0, slot0, wave * GPL, steps);
+    if constexpr (XLDS) {
 #pragma unroll
-            for (int t = 0; t < 4; ++t) a[t] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+        for (int r = 0; r < kXVecs; ++r) {
+            const int i = threadIdx.x + r * kThreads;
+            if (i < M * vpr) *reinterpret_cast<uint4*>(xs + 8 * i) = xv[r];
         }
-        if constexpr (MODE == kModeRaw) {
-            half8 b[4];
-            if (row_ok && g_ok) {
-                load_w16(m, g, b);
-            } else {
-#pragma unroll
-                for (int t = 0; t < 4; ++t) b[t] = half8{0, 0, 0, 0, 0, 0, 0, 0};
-            }
-#pragma unroll
-            for (int t = 0; t < 4; ++t) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], b[t], acc, 0, 0, 0);
-        } else {
-            Raw<B> r;
-            if (row_ok && g_ok) raw_load<B>(m, g, r); else raw_zero<B>(r);
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const half8 b = decode8<B, MODE>(r, t, s);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], b, acc, 0, 0, 0);
-            }
+        __syncthreads();
+    }
+    auto batch = [&](const Bits (&cur)[GPL], Bits (&nxt)[GPL], bool prefetch, int bi) {
+        decode_activations<GPL, XLDS>(a, m, bi * kBatch, wave, quarter, m_ok, steps, xrow, xsrow, xvec);
+        if (prefetch) decode_load_batch<GPL>(m, nxt, slot0, (bi + 1) * kBatch + wave * GPL, steps);
+        decode_mul_batch<B, MODE, GPL>(cur, a, bi * kBatch + wave * GPL, steps, s, acc);
+    };
+    for (int bi = 0;; bi += 2) {
+        if (bi + 1 >= nb) {
+            batch(buf0, buf1, false, bi);
+            break;
         }
+        batch(buf0, buf1, true, bi);
+        if (bi + 2 >= nb) {
+            batch(buf1, buf0, false, bi + 1);
+            break;
+        }
+        batch(buf1, buf0, true, bi + 1);
     }
 
     // cross-wave reduction of the 16x16 fp32 tile
     __shared__ floatx4 red[WAVES][64];
     red[wave][lane] = acc;
     __syncthreads();
-    for (int o = threadIdx.x; o < 256; o += 64 * WAVES) {
-        const int src = o & 63;
-        const int e = o >> 6;
+    if (threadIdx.x < 256) {
+        const int src = threadIdx.x & 63;
+        const int e = threadIdx.x >> 6;
         float v = 0.0f;
 #pragma unroll
         for (int w = 0; w < WAVES; ++w) v += red[w][src][e];
         const int mi = 4 * (src >> 4) + e;           // D[4*(l/16)+e][l%16]
-        const int n = blockIdx.x * 16 + (src & 15);
-        if (mi < M && n < m.rows) {
-            float sn = 1.0f;
-            if constexpr (MODE == kModeQ) sn = m.scales[n];
-            y[static_cast<size_t>(mi) * m.rows + n] = epilogue<MODE>(v, sn, bias, n);
+        if (mi < M && on < m.rows) {
+            y[static_cast<size_t>(mi) * m.rows + on] =
+                epilogue<MODE>(v, out_scale, bias != nullptr, out_bias);
         }
     }
 }
@@ -464,7 +622,7 @@ __global__ __launch_bounds__(256) void linear_gemm_kernel(
         }
         const int grp = 2 * kt + wh;
         const bool ok = wrow_ok && grp < m.gpr;
-        const size_t g = static_cast<size_t>(wrow) * m.gpr + grp;
+        const size_t g = group_slot(wrow, grp, m.spr);
         if constexpr (MODE == kModeRaw) {
             if (ok) {
                 const uint4* p = reinterpret_cast<const uint4*>(m.w16 + g * kGroup);
@@ -535,12 +693,13 @@ __global__ __launch_bounds__(256) void linear_gemm_kernel(
         if (n >= m.rows) continue;
         float sn = 1.0f;
         if constexpr (MODE == kModeQ) sn = m.scales[n];
+        const uint16_t bn = bias ? bias[n] : uint16_t(0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int r = m0 + wm * 64 + 16 * i + 4 * (lane >> 4) + e;
-                if (r < M) y[static_cast<size_t>(r) * m.rows + n] = epilogue<MODE>(acc[i][j][e], sn, bias, n);
+                if (r < M) y[static_cast<size_t>(r) * m.rows + n] = epilogue<MODE>(acc[i][j][e], sn, bias != nullptr, bn);
             }
         }
     }
@@ -647,9 +806,9 @@ hipError_t dispatch_bits(int bits, Args&&... args) {
 template <int B>
 struct RepackOp {
     static hipError_t run(const uint8_t* canon, uint64_t canon_bytes, const DevMatrixOut& out, hipStream_t s) {
-        const uint64_t groups = static_cast<uint64_t>(out.rows) * out.gpr;
-        hipLaunchKernelGGL(repack_kernel<B>, dim3(blocks_for(groups, 256)), dim3(256), 0, s,
-                           canon, canon_bytes, out, groups);
+        const uint64_t slots = static_cast<uint64_t>(out.rtiles) * out.spr * kTileSlots;
+        hipLaunchKernelGGL(repack_kernel<B>, dim3(blocks_for(slots, 256)), dim3(256), 0, s,
+                           canon, canon_bytes, out, slots);
         return hipGetLastError();
     }
 };
@@ -657,8 +816,8 @@ struct RepackOp {
 template <int B>
 struct UnpackOp {
     static hipError_t run(const DevMatrix& m, int16_t* out, hipStream_t s) {
-        const uint64_t groups = static_cast<uint64_t>(m.rows) * m.gpr;
-        hipLaunchKernelGGL(unpack_kernel<B>, dim3(blocks_for(groups, 256)), dim3(256), 0, s, m, out, groups);
+        const uint64_t slots = static_cast<uint64_t>(m.rtiles) * m.spr * kTileSlots;
+        hipLaunchKernelGGL(unpack_kernel<B>, dim3(blocks_for(slots, 256)), dim3(256), 0, s, m, out, slots);
         return hipGetLastError();
     }
 };
@@ -666,22 +825,35 @@ struct UnpackOp {
 template <int B>
 struct MaterializeOp {
     static hipError_t run(const DevMatrix& m, uint16_t* out, hipStream_t s) {
-        const uint64_t groups = static_cast<uint64_t>(m.rows) * m.gpr;
-        hipLaunchKernelGGL(materialize_kernel<B>, dim3(blocks_for(groups, 256)), dim3(256), 0, s, m, out,
-                           groups);
+        const uint64_t slots = static_cast<uint64_t>(m.rtiles) * m.spr * kTileSlots;
+        hipLaunchKernelGGL(materialize_kernel<B>, dim3(blocks_for(slots, 256)), dim3(256), 0, s, m, out,
+                           slots);
         return hipGetLastError();
     }
 };
 
-constexpr int kSkinnyWaves = 8;
-constexpr int kSkinnyMaxM = 16;
+#ifndef EBK_DECODE_WAVES
+#define EBK_DECODE_WAVES 8
+#endif
+#ifndef EBK_DECODE_GPL
+#define EBK_DECODE_GPL 1
+#endif
+constexpr int kDecodeWaves = EBK_DECODE_WAVES;
+constexpr int kDecodeGpl = EBK_DECODE_GPL;
+constexpr int kDecodeMaxM = 16;
 
 template <int B, int MODE>
 hipError_t run_linear_mode(const DevMatrix& m, const uint16_t* x, int64_t M, uint16_t* y,
                            const uint16_t* bias, int xvec, hipStream_t s) {
-    if (M <= kSkinnyMaxM) {
-        hipLaunchKernelGGL((linear_skinny_kernel<B, MODE, kSkinnyWaves>), dim3((m.rows + 15) / 16),
-                           dim3(64 * kSkinnyWaves), 0, s, m, x, static_cast<int>(M), y, bias, xvec);
+    if (M <= kDecodeMaxM) {
+        const size_t xbytes = static_cast<size_t>(M) * m.spr * kTileGroups * kGroup * 2;
+        if (xbytes <= static_cast<size_t>(kXLdsBytes)) {
+            hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, true>), dim3(m.rtiles),
+                               dim3(64 * kDecodeWaves), xbytes, s, m, x, static_cast<int>(M), y, bias, xvec);
+        } else {
+            hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, false>), dim3(m.rtiles),
+                               dim3(64 * kDecodeWaves), 0, s, m, x, static_cast<int>(M), y, bias, xvec);
+        }
     } else {
         const dim3 grid((m.rows + kBN - 1) / kBN, static_cast<unsigned>((M + kBM - 1) / kBM));
         hipLaunchKernelGGL((linear_gemm_kernel<B, MODE>), grid, dim3(256), 0, s, m, x,
@@ -710,9 +882,9 @@ struct LinearOp {
 hipError_t launch_repack(const uint8_t* canon, uint64_t canon_bytes, const DevMatrixOut& out,
                          hipStream_t stream) {
     if (out.bits == 16) {
-        const uint64_t groups = static_cast<uint64_t>(out.rows) * out.gpr;
-        hipLaunchKernelGGL(repack16_kernel, dim3(blocks_for(groups, 256)), dim3(256), 0, stream,
-                           reinterpret_cast<const uint16_t*>(canon), out, groups);
+        const uint64_t slots = static_cast<uint64_t>(out.rtiles) * out.spr * kTileSlots;
+        hipLaunchKernelGGL(repack16_kernel, dim3(blocks_for(slots, 256)), dim3(256), 0, stream,
+                           reinterpret_cast<const uint16_t*>(canon), out, slots);
         return hipGetLastError();
     }
     return dispatch_bits<RepackOp>(out.bits, canon, canon_bytes, out, stream);
