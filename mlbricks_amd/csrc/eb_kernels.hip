@@ -78,6 +78,32 @@ __device__ __forceinline__ void raw_load(const DevMatrix& m, size_t g, Raw<B>& r
     }
 }
 
+// raw_load with a 32-bit slot index: the planes of one matrix stay below
+// 4 GiB, so each address is a scalar base plus a 32-bit vector byte offset
+// (the saddr form of global_load) instead of 64-bit vector arithmetic.
+template <int B>
+__device__ __forceinline__ void raw_load32(const DevMatrix& m, uint32_t g, Raw<B>& r) {
+    using P = Planes<B>;
+    if constexpr (P::h8) {
+        const uint8_t* p = m.p8 + g * 32u;
+        const uint4 a = *reinterpret_cast<const uint4*>(p);
+        const uint4 b = *reinterpret_cast<const uint4*>(p + 16);
+        r.d8[0] = a.x; r.d8[1] = a.y; r.d8[2] = a.z; r.d8[3] = a.w;
+        r.d8[4] = b.x; r.d8[5] = b.y; r.d8[6] = b.z; r.d8[7] = b.w;
+    }
+    if constexpr (P::h4) {
+        const uint4 a = *reinterpret_cast<const uint4*>(m.p4 + g * 16u);
+        r.d4[0] = a.x; r.d4[1] = a.y; r.d4[2] = a.z; r.d4[3] = a.w;
+    }
+    if constexpr (P::h2) {
+        const uint2 a = *reinterpret_cast<const uint2*>(m.p2 + g * 8u);
+        r.d2[0] = a.x; r.d2[1] = a.y;
+    }
+    if constexpr (P::h1) {
+        r.d1 = *reinterpret_cast<const uint32_t*>(m.p1 + g * 4u);
+    }
+}
+
 // Quad d (codes 4d..4d+3) as byte lanes: lo = bits 0..7 of each u, hi = bits 8+.
 template <int B>
 __device__ __forceinline__ void quad_bytes(const Raw<B>& r, int d, uint32_t& lo, uint32_t& hi) {
@@ -106,6 +132,8 @@ __device__ __forceinline__ uint32_t pack_h2(_Float16 a, _Float16 b) {
 template <int B>
 __device__ __forceinline__ void quad_q(uint32_t lo, uint32_t hi, uint32_t& w0, uint32_t& w1) {
     static_assert(B <= 10, "fp16 mantissa holds at most 10 code bits");
+    // hi holds only bits the byte mask 0x03030303 (or narrower) keeps, so
+    // OR-ing in the exponent byte 0x64 is a bit-field insert.
     const uint32_t H = hi | 0x64646464u;
     const uint32_t a = __builtin_amdgcn_perm(H, lo, 0x05010400u);  // [lo0 H0 lo1 H1]
     const uint32_t b = __builtin_amdgcn_perm(H, lo, 0x07030602u);  // [lo2 H2 lo3 H3]
@@ -364,6 +392,7 @@ template <int B, int MODE>
 struct GroupBits {
     Raw<B> r;
     __device__ __forceinline__ void load(const DevMatrix& m, size_t g) { raw_load<B>(m, g, r); }
+    __device__ __forceinline__ void load32(const DevMatrix& m, uint32_t g) { raw_load32<B>(m, g, r); }
     __device__ __forceinline__ half8 operand(int t, float s) const { return decode8<B, MODE>(r, t, s); }
 };
 
@@ -706,6 +735,293 @@ __global__ __launch_bounds__(256) void linear_gemm_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// prefill kernel (tiled planes), M > 16, integer-dot and decoded-fp16 modes.
+//
+// Workgroup tile: 128 activation rows x 256 weight rows (16 row tiles), K
+// steps of 128 columns (one plane tile).  Each of the four waves owns 64
+// weight rows (four row tiles) for all 128 activation rows: a 128 x 64
+// accumulator tile, 4 x 2 blocks of v_mfma_f32_32x32x16_f16 (the 32x32
+// shape sustains near-peak rate with few independent accumulators; the
+// 16x16x32 shape needs many more).
+//
+//  * B (weights) never goes through LDS.  For weight block nb2 (32 rows =
+//    two row tiles) and group pair p, lane l = 32h + n loads slot
+//    16*(2p+h) + n%16 of row tile 2*nb2 + n/16 -- the B operand rows of
+//    v_mfma_f32_32x32x16_f16 -- and decodes it in registers.  Each decoded
+//    operand feeds four MFMAs (one per 32 activation rows).  B of step k+1
+//    is loaded into a second register buffer while step k is multiplied.
+//  * A (activations) goes global -> LDS directly (global_load_lds_dwordx4,
+//    no registers), into a ring of three stages so that step k+2 is in
+//    flight while step k is multiplied.  A stage row is 256 bytes with its
+//    16-byte chunks XOR-swizzled by (row & 15), so a wave's operand reads
+//    (16 consecutive rows, one chunk per half wave) hit every bank once.
+//  * The K order inside a step is the same for both operands: MFMA (p, t)
+//    takes codes 8t..8t+8 of group 2p+h in lane half h, i.e. columns
+//    32*(2p+h) + 8t + i.
+//  * Loads are unconditional: past the last step the clamped address
+//    re-reads the last step (L2 hits), so no wait covers loads behind a
+//    branch.  Rows past M read the last row; their outputs are not stored.
+//  * Workgroup -> tile: dispatch places workgroup i on XCD i % 8, so each
+//    XCD is given a contiguous range of tiles, walked four activation blocks
+//    at a time, and the ~32 workgroups an XCD runs at once share their
+//    activation and weight blocks in that XCD's L2.
+// ---------------------------------------------------------------------------
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int kPM = 128;                   // activation rows per workgroup
+constexpr int kPN = 256;                   // weight rows per workgroup (4 waves x 64)
+constexpr int kPK = kTileGroups * kGroup;  // 128 columns per step
+constexpr int kPRow = kPK * 2;             // bytes per staged activation row
+constexpr int kPStage = kPM * kPRow;       // bytes per stage (32 KB)
+constexpr int kPStages = 3;
+constexpr int kPGroupM = 4;                // activation blocks per tile-order group
+
+// Workgroup barrier for the direct-to-LDS pipeline.  __syncthreads() opens
+// with a release fence, which waits for every outstanding vector load --
+// including the prefetch that should stay in flight across the barrier.
+// The caller waits for the loads the next step reads (wait_vmcnt) and the
+// barrier keeps only the acquire side.  Prior LDS reads have all returned:
+// their MFMAs consumed them.
+__device__ __forceinline__ void barrier_after_wait() {
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// s_waitcnt with only the LDS / scalar-memory counter constrained.
+template <int N>
+__device__ __forceinline__ void wait_lgkmcnt() {
+    static_assert(N >= 0 && N < 16, "lgkmcnt is a 4-bit counter");
+    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4) | (N << 8));
+}
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int B, int MODE>
+__global__ __launch_bounds__(256) void linear_prefill_kernel(
+    DevMatrix m, const uint16_t* __restrict__ x, int M, uint16_t* __restrict__ y,
+    const uint16_t* __restrict__ bias, int mblocks, int nblocks, int per_xcd) {
+    static_assert(MODE != kModeRaw, "raw fp16 weights use linear_gemm_kernel");
+    using Bits = GroupBits<B, MODE>;
+    constexpr int kALoads = 8;                       // A loads per step per wave
+    __shared__ __attribute__((aligned(16))) uint8_t xs[kPStages * kPStage];
+
+    // ---- tile of this workgroup (uniform early exit, before any barrier) ----
+    const int xcd = blockIdx.x & 7;
+    const int local = blockIdx.x >> 3;
+    const int tile = xcd * per_xcd + local;
+    if (local >= per_xcd || tile >= mblocks * nblocks) return;
+    const int group = tile / (kPGroupM * nblocks);
+    const int within = tile - group * kPGroupM * nblocks;
+    const int gm = min(kPGroupM, mblocks - group * kPGroupM);
+    const int mb = group * kPGroupM + within % gm;
+    const int nb = within / gm;
+    const int m0 = mb * kPM;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n32 = lane & 31;
+    const int half = lane >> 5;
+    const int steps = m.spr;
+
+    // B slots of this lane: [nb2][p] -> row tile 2*nb2 + n32/16 of the wave,
+    // slot 16*(2p + half) + n32%16 (row tiles clamped; rows past the end are
+    // never stored).  Slot indices fit 32 bits (planes below 4 GiB).
+    uint32_t slot0[2][2];
+    float s[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int nb2 = 0; nb2 < 2; ++nb2) {
+        const int rt = min(nb * (kPN / kTileRows) + wave * 4 + 2 * nb2 + (n32 >> 4), m.rtiles - 1);
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            slot0[nb2][p] = static_cast<uint32_t>(rt) * static_cast<uint32_t>(steps * kTileSlots) +
+                            static_cast<uint32_t>(16 * (2 * p + half) + (n32 & 15));
+        }
+        if constexpr (MODE == kModeW) {
+            const int row = rt * kTileRows + (n32 & 15);
+            s[nb2] = row < m.rows ? m.scales[row] : 0.0f;
+        }
+    }
+
+    // Activation loads of step st into stage `stage`: wave w fills rows
+    // 32w .. 32w+31, four rows (1 KB, one instruction) at a time; lane l
+    // writes physical chunk l%16 of row l/16, i.e. logical chunk
+    // (l%16) ^ (row & 15).  Per lane and instruction the source is a fixed
+    // row (clamped to M-1) and a fixed chunk; only the column base moves.
+    // The launcher guarantees cols % 8 == 0, a 16-byte aligned x and
+    // M * cols * 2 below 4 GiB.
+    uint32_t arow[kALoads];
+    int achunk[kALoads];
+#pragma unroll
+    for (int i = 0; i < kALoads; ++i) {
+        const int r = wave * 32 + i * 4 + (lane >> 4);
+        achunk[i] = 8 * ((lane & 15) ^ (r & 15));
+        arow[i] = static_cast<uint32_t>(min(m0 + r, M - 1)) * static_cast<uint32_t>(m.cols);
+    }
+    const uint8_t* xb = reinterpret_cast<const uint8_t*>(x);
+    auto load_a = [&](int st, int stage) {
+        const int k0 = min(st, steps - 1) * kPK;
+        const int kmax = m.cols - 8;
+#pragma unroll
+        for (int i = 0; i < kALoads; ++i) {
+            const uint32_t off = 2u * (arow[i] + static_cast<uint32_t>(min(k0 + achunk[i], kmax)));
+            __builtin_amdgcn_global_load_lds(xb + off, xs + stage * kPStage + (wave * 32 + i * 4) * kPRow, 16, 0, 0);
+        }
+    };
+    auto load_b = [&](Bits (&bits)[2][2], int st) {
+        const uint32_t off = static_cast<uint32_t>(min(st, steps - 1) * kTileSlots);
+#pragma unroll
+        for (int nb2 = 0; nb2 < 2; ++nb2)
+#pragma unroll
+            for (int p = 0; p < 2; ++p) bits[nb2][p].load32(m, slot0[nb2][p] + off);
+    };
+
+    floatx16 acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    // A operands of MFMA (p, t) for the four 32-row blocks: row 32i + n32,
+    // logical chunk 4*(2p + half) + t.
+    auto read_a = [&](half8 (&a)[4], int stage, int p, int t) {
+        const int chunk = (4 * (2 * p + half) + t) ^ (n32 & 15);
+        const uint8_t* base = xs + stage * kPStage + n32 * kPRow + chunk * 16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const half8*>(base + 32 * i * kPRow);
+    };
+    // Slices pt = 0..7 of a step (group pair p = pt/4, codes t = pt%4).
+    // Software pipeline per slice: read the A operands of slice pt+1 from
+    // LDS and decode the B operands of slice pt+1 while the eight MFMAs of
+    // slice pt run, then wait for the reads.  sched_barrier pins the slice
+    // boundaries; inside a slice the compiler interleaves the decode VALU
+    // with the MFMAs.
+    auto decode_pt = [&](const Bits (&cur)[2][2], half8 (&bop)[2], int pt) {
+#pragma unroll
+        for (int nb2 = 0; nb2 < 2; ++nb2) bop[nb2] = cur[nb2][pt >> 2].operand(pt & 3, s[nb2]);
+    };
+    auto mfma_pt = [&](const half8 (&a)[4], const half8 (&bop)[2]) {
+#pragma unroll
+        for (int nb2 = 0; nb2 < 2; ++nb2) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                acc[i][nb2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bop[nb2], acc[i][nb2], 0, 0, 0);
+            }
+        }
+    };
+    auto multiply = [&](const Bits (&cur)[2][2], int stage) {
+        half8 a0[4], a1[4];
+        half8 b0[2], b1[2];
+        read_a(a0, stage, 0, 0);
+        decode_pt(cur, b0, 0);
+        wait_lgkmcnt<0>();
+#pragma unroll
+        for (int pt = 0; pt < 8; pt += 2) {
+            read_a(a1, stage, (pt + 1) >> 2, (pt + 1) & 3);
+            decode_pt(cur, b1, pt + 1);
+            mfma_pt(a0, b0);
+            __builtin_amdgcn_sched_barrier(0);
+            wait_lgkmcnt<0>();
+            if (pt + 2 < 8) {
+                read_a(a0, stage, (pt + 2) >> 2, (pt + 2) & 3);
+                decode_pt(cur, b0, pt + 2);
+            }
+            mfma_pt(a1, b1);
+            __builtin_amdgcn_sched_barrier(0);
+            wait_lgkmcnt<0>();
+        }
+    };
+
+    // Issue order matters (vector loads retire in order).  Per step: B of
+    // step st+1, then A of step st+2.  Before the barrier the wave waits for
+    // everything except the A batch just issued, i.e. for A(st+1) and
+    // B(st+1).  sched_barrier keeps the compiler from sinking the loads into
+    // the multiply.
+    Bits b0[2][2], b1[2][2];
+    load_b(b0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    load_a(0, 0);
+    load_a(1, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmcnt<kALoads>();         // B(0) and A(0) landed; A(1) in flight
+    barrier_after_wait();
+    // One step: load B(st+1) into `next`, A(st+2); multiply B(st) held in
+    // `cur`; wait for A(st+1) and B(st+1); barrier.  The two B buffers swap
+    // roles by unrolling, so no register copy is needed.
+    auto step = [&](const Bits (&cur)[2][2], Bits (&next)[2][2], int st) {
+        load_b(next, st + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        load_a(st + 2, (st + 2) % kPStages);
+        __builtin_amdgcn_sched_barrier(0);
+        multiply(cur, st % kPStages);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt<kALoads>();     // A(st+1) and B(st+1) landed; A(st+2) in flight
+        barrier_after_wait();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    for (int st = 0;; st += 2) {
+        step(b0, b1, st);
+        if (st + 1 >= steps) break;
+        step(b1, b0, st + 1);
+        if (st + 2 >= steps) break;
+    }
+
+    // ---- epilogue ----
+    // 32x32 block element e of lane l is D[8*(e/4) + 4*(l/32) + e%4][l%32].
+    // Each wave converts its 128 x 64 tile to fp16 (scale, rounding, bias)
+    // into its own LDS region, then writes it back row by row with 16-byte
+    // stores, eight lanes per 128-byte row segment.  The A stages are free by
+    // now; the clamped re-reads of the last steps must land before the
+    // region is reused.
+    wait_vmcnt<0>();
+    __syncthreads();
+    constexpr int kCPitch = 144;                 // bytes per staged output row (128 + 16)
+    uint8_t* cw = xs + wave * (kPM * kCPitch);
+    const int nw0 = nb * kPN + wave * 64;        // first weight row of this wave
+#pragma unroll
+    for (int nb2 = 0; nb2 < 2; ++nb2) {
+        const int n = min(nw0 + 32 * nb2 + n32, m.rows - 1);
+        float sn = 1.0f;
+        if constexpr (MODE == kModeQ) sn = m.scales[n];
+        const uint16_t bn = bias ? bias[n] : uint16_t(0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int r = 32 * i + 8 * (e >> 2) + 4 * half + (e & 3);
+                *reinterpret_cast<uint16_t*>(cw + r * kCPitch + (32 * nb2 + n32) * 2) =
+                    epilogue<MODE>(acc[i][nb2][e], sn, bias != nullptr, bn);
+            }
+        }
+    }
+    __syncthreads();
+    const bool yvec = (m.rows % 8 == 0) && (reinterpret_cast<uintptr_t>(y) % 16 == 0);
+    const int chunk = lane & 7;
+#pragma unroll 4
+    for (int it = 0; it < kPM / 8; ++it) {
+        const int r = it * 8 + (lane >> 3);
+        const int gr = m0 + r;
+        const int gn = nw0 + chunk * 8;
+        if (gr >= M || gn >= m.rows) continue;
+        const uint4 v = *reinterpret_cast<const uint4*>(cw + r * kCPitch + chunk * 16);
+        uint16_t* dst = y + static_cast<size_t>(gr) * m.rows + gn;
+        if (yvec) {
+            *reinterpret_cast<uint4*>(dst) = v;
+        } else {
+            const uint16_t* h = reinterpret_cast<const uint16_t*>(&v);
+            for (int k = 0; k < 8 && gn + k < m.rows; ++k) dst[k] = h[k];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // legacy flat-group op (bolt/ops_cuda.cu:2708-2750): one wave per output
 // feature, four activation rows per wave, lanes stride over K.
 // ---------------------------------------------------------------------------
@@ -853,6 +1169,14 @@ hipError_t run_linear_mode(const DevMatrix& m, const uint16_t* x, int64_t M, uin
         } else {
             hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, false>), dim3(m.rtiles),
                                dim3(64 * kDecodeWaves), 0, s, m, x, static_cast<int>(M), y, bias, xvec);
+        }
+    } else if (MODE != kModeRaw && xvec && static_cast<uint64_t>(M) * m.cols * 2 < (uint64_t(1) << 32)) {
+        if constexpr (MODE != kModeRaw) {
+            const int mblocks = static_cast<int>((M + kPM - 1) / kPM);
+            const int nblocks = (m.rows + kPN - 1) / kPN;
+            const int per_xcd = (mblocks * nblocks + 7) / 8;
+            hipLaunchKernelGGL((linear_prefill_kernel<B, MODE>), dim3(8 * per_xcd), dim3(256), 0, s, m, x,
+                               static_cast<int>(M), y, bias, mblocks, nblocks, per_xcd);
         }
     } else {
         const dim3 grid((m.rows + kBN - 1) / kBN, static_cast<unsigned>((M + kBM - 1) / kBM));
