@@ -769,13 +769,31 @@ __global__ __launch_bounds__(256) void linear_gemm_kernel(
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int kPM = 128;                   // activation rows per workgroup
 constexpr int kPN = 256;                   // weight rows per workgroup (4 waves x 64)
 constexpr int kPK = kTileGroups * kGroup;  // 128 columns per step
 constexpr int kPRow = kPK * 2;             // bytes per staged activation row
-constexpr int kPStage = kPM * kPRow;       // bytes per stage (32 KB)
-constexpr int kPStages = 3;
 constexpr int kPGroupM = 4;                // activation blocks per tile-order group
+
+// An LDS address as the address-space-3 pointer global_load_lds takes.  The
+// explicit cast at the call matters: without it hipcc's host pass silently
+// drops the launch stub of a kernel template that passes an LDS array
+// expression of dependent type to the builtin (and a __device__ helper doing
+// the cast has the same effect).
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+
+// Prefill tile geometry for MI 32-row activation blocks per wave.
+template <int MI>
+struct PrefillShape {
+    // 256 rows (MI = 8) needs 256 accumulator registers per lane; that build
+    // spilled and did not reproduce the oracle, so only 128 rows is enabled.
+    static_assert(MI == 4, "the prefill kernel is built for 128 activation rows per workgroup");
+    static constexpr int kRows = 32 * MI;            // activation rows per workgroup
+    static constexpr int kStage = kRows * kPRow;     // bytes per activation stage
+    static constexpr int kStages = MI == 4 ? 3 : 2;  // 96 KB or 128 KB of LDS
+    static constexpr int kLds = kStages * kStage;
+    static constexpr int kALoads = kRows / 16;       // A loads per step per wave (1 KB each)
+    static constexpr int kADist = kStages - 1;       // activation prefetch distance
+};
 
 // Workgroup barrier for the direct-to-LDS pipeline.  __syncthreads() opens
 // with a release fence, which waits for every outstanding vector load --
@@ -802,26 +820,33 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <int B, int MODE>
+template <int B, int MODE, int MI, int NB>
 __global__ __launch_bounds__(256) void linear_prefill_kernel(
     DevMatrix m, const uint16_t* __restrict__ x, int M, uint16_t* __restrict__ y,
-    const uint16_t* __restrict__ bias, int mblocks, int nblocks, int per_xcd) {
+    const uint16_t* __restrict__ bias, int mblocks, int nblocks, int tile0, int njobs, int per_xcd) {
     static_assert(MODE != kModeRaw, "raw fp16 weights use linear_gemm_kernel");
     using Bits = GroupBits<B, MODE>;
-    constexpr int kALoads = 8;                       // A loads per step per wave
-    __shared__ __attribute__((aligned(16))) uint8_t xs[kPStages * kPStage];
+    using Shape = PrefillShape<MI>;
+    __shared__ __attribute__((aligned(16))) uint8_t xs[Shape::kLds];
 
+    static_assert(NB == 1 || NB == 2, "32 or 64 weight rows per wave");
     // ---- tile of this workgroup (uniform early exit, before any barrier) ----
+    // Jobs j = 0 .. njobs-1 cover the full tiles tile0, tile0+1, ... of the
+    // grouped order (128 x 256); with NB = 1 two jobs split a full tile into
+    // its two 128-row weight halves.
     const int xcd = blockIdx.x & 7;
     const int local = blockIdx.x >> 3;
-    const int tile = xcd * per_xcd + local;
-    if (local >= per_xcd || tile >= mblocks * nblocks) return;
+    const int job = xcd * per_xcd + local;
+    if (local >= per_xcd || job >= njobs) return;
+    const int tile = tile0 + (NB == 2 ? job : job >> 1);
     const int group = tile / (kPGroupM * nblocks);
     const int within = tile - group * kPGroupM * nblocks;
     const int gm = min(kPGroupM, mblocks - group * kPGroupM);
     const int mb = group * kPGroupM + within % gm;
     const int nb = within / gm;
-    const int m0 = mb * kPM;
+    const int m0 = mb * Shape::kRows;
+    // first weight row of this workgroup and of this wave
+    const int n0 = nb * kPN + (NB == 2 ? 0 : (job & 1) * (kPN / 2));
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -829,14 +854,16 @@ __global__ __launch_bounds__(256) void linear_prefill_kernel(
     const int half = lane >> 5;
     const int steps = m.spr;
 
+    const int nw0 = n0 + wave * 32 * NB;
     // B slots of this lane: [nb2][p] -> row tile 2*nb2 + n32/16 of the wave,
     // slot 16*(2p + half) + n32%16 (row tiles clamped; rows past the end are
     // never stored).  Slot indices fit 32 bits (planes below 4 GiB).
-    uint32_t slot0[2][2];
-    float s[2] = {0.0f, 0.0f};
+    uint32_t slot0[NB][2];
+    float s[NB];
 #pragma unroll
-    for (int nb2 = 0; nb2 < 2; ++nb2) {
-        const int rt = min(nb * (kPN / kTileRows) + wave * 4 + 2 * nb2 + (n32 >> 4), m.rtiles - 1);
+    for (int nb2 = 0; nb2 < NB; ++nb2) {
+        s[nb2] = 0.0f;
+        const int rt = min(nw0 / kTileRows + 2 * nb2 + (n32 >> 4), m.rtiles - 1);
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
             slot0[nb2][p] = static_cast<uint32_t>(rt) * static_cast<uint32_t>(steps * kTileSlots) +
@@ -849,53 +876,55 @@ __global__ __launch_bounds__(256) void linear_prefill_kernel(
     }
 
     // Activation loads of step st into stage `stage`: wave w fills rows
-    // 32w .. 32w+31, four rows (1 KB, one instruction) at a time; lane l
+    // w*Shape::kRows/4 .. (w+1)*Shape::kRows/4 - 1, four rows (1 KB, one instruction) at a time; lane l
     // writes physical chunk l%16 of row l/16, i.e. logical chunk
     // (l%16) ^ (row & 15).  Per lane and instruction the source is a fixed
     // row (clamped to M-1) and a fixed chunk; only the column base moves.
     // The launcher guarantees cols % 8 == 0, a 16-byte aligned x and
     // M * cols * 2 below 4 GiB.
-    uint32_t arow[kALoads];
-    int achunk[kALoads];
+    // Instruction i covers rows w*Shape::kRows/4 + 4i + l/16; its chunk pattern
+    // repeats every four instructions.
+    int achunk[4];
 #pragma unroll
-    for (int i = 0; i < kALoads; ++i) {
-        const int r = wave * 32 + i * 4 + (lane >> 4);
-        achunk[i] = 8 * ((lane & 15) ^ (r & 15));
-        arow[i] = static_cast<uint32_t>(min(m0 + r, M - 1)) * static_cast<uint32_t>(m.cols);
-    }
+    for (int i = 0; i < 4; ++i) achunk[i] = 8 * ((lane & 15) ^ ((4 * i + (lane >> 4)) & 15));
+    const int arow0 = m0 + wave * (Shape::kRows / 4) + (lane >> 4);
     const uint8_t* xb = reinterpret_cast<const uint8_t*>(x);
     auto load_a = [&](int st, int stage) {
         const int k0 = min(st, steps - 1) * kPK;
         const int kmax = m.cols - 8;
 #pragma unroll
-        for (int i = 0; i < kALoads; ++i) {
-            const uint32_t off = 2u * (arow[i] + static_cast<uint32_t>(min(k0 + achunk[i], kmax)));
-            __builtin_amdgcn_global_load_lds(xb + off, xs + stage * kPStage + (wave * 32 + i * 4) * kPRow, 16, 0, 0);
+        for (int i = 0; i < Shape::kALoads; ++i) {
+            const uint32_t row = static_cast<uint32_t>(min(arow0 + 4 * i, M - 1));
+            const uint32_t off = 2u * (row * static_cast<uint32_t>(m.cols) +
+                                       static_cast<uint32_t>(min(k0 + achunk[i & 3], kmax)));
+            __builtin_amdgcn_global_load_lds(xb + off, (lds_void_ptr)(xs + stage * Shape::kStage +
+                                                                      (wave * (Shape::kRows / 4) + i * 4) * kPRow),
+                                             16, 0, 0);
         }
     };
-    auto load_b = [&](Bits (&bits)[2][2], int st) {
+    auto load_b = [&](Bits (&bits)[NB][2], int st) {
         const uint32_t off = static_cast<uint32_t>(min(st, steps - 1) * kTileSlots);
 #pragma unroll
-        for (int nb2 = 0; nb2 < 2; ++nb2)
+        for (int nb2 = 0; nb2 < NB; ++nb2)
 #pragma unroll
             for (int p = 0; p < 2; ++p) bits[nb2][p].load32(m, slot0[nb2][p] + off);
     };
 
-    floatx16 acc[4][2];
+    floatx16 acc[MI][NB];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < NB; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    // A operands of MFMA (p, t) for the four 32-row blocks: row 32i + n32,
+    // A operands of MFMA (p, t) for the MI 32-row blocks: row 32i + n32,
     // logical chunk 4*(2p + half) + t.
-    auto read_a = [&](half8 (&a)[4], int stage, int p, int t) {
+    auto read_a = [&](half8 (&a)[MI], int stage, int p, int t) {
         const int chunk = (4 * (2 * p + half) + t) ^ (n32 & 15);
-        const uint8_t* base = xs + stage * kPStage + n32 * kPRow + chunk * 16;
+        const uint8_t* base = xs + stage * Shape::kStage + n32 * kPRow + chunk * 16;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const half8*>(base + 32 * i * kPRow);
+        for (int i = 0; i < MI; ++i) a[i] = *reinterpret_cast<const half8*>(base + 32 * i * kPRow);
     };
     // Slices pt = 0..7 of a step (group pair p = pt/4, codes t = pt%4).
     // Software pipeline per slice: read the A operands of slice pt+1 from
@@ -903,22 +932,22 @@ __global__ __launch_bounds__(256) void linear_prefill_kernel(
     // slice pt run, then wait for the reads.  sched_barrier pins the slice
     // boundaries; inside a slice the compiler interleaves the decode VALU
     // with the MFMAs.
-    auto decode_pt = [&](const Bits (&cur)[2][2], half8 (&bop)[2], int pt) {
+    auto decode_pt = [&](const Bits (&cur)[NB][2], half8 (&bop)[NB], int pt) {
 #pragma unroll
-        for (int nb2 = 0; nb2 < 2; ++nb2) bop[nb2] = cur[nb2][pt >> 2].operand(pt & 3, s[nb2]);
+        for (int nb2 = 0; nb2 < NB; ++nb2) bop[nb2] = cur[nb2][pt >> 2].operand(pt & 3, s[nb2]);
     };
-    auto mfma_pt = [&](const half8 (&a)[4], const half8 (&bop)[2]) {
+    auto mfma_pt = [&](const half8 (&a)[MI], const half8 (&bop)[NB]) {
 #pragma unroll
-        for (int nb2 = 0; nb2 < 2; ++nb2) {
+        for (int nb2 = 0; nb2 < NB; ++nb2) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < MI; ++i) {
                 acc[i][nb2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bop[nb2], acc[i][nb2], 0, 0, 0);
             }
         }
     };
-    auto multiply = [&](const Bits (&cur)[2][2], int stage) {
-        half8 a0[4], a1[4];
-        half8 b0[2], b1[2];
+    auto multiply = [&](const Bits (&cur)[NB][2], int stage) {
+        half8 a0[MI], a1[MI];
+        half8 b0[NB], b1[NB];
         read_a(a0, stage, 0, 0);
         decode_pt(cur, b0, 0);
         wait_lgkmcnt<0>();
@@ -944,25 +973,25 @@ __global__ __launch_bounds__(256) void linear_prefill_kernel(
     // everything except the A batch just issued, i.e. for A(st+1) and
     // B(st+1).  sched_barrier keeps the compiler from sinking the loads into
     // the multiply.
-    Bits b0[2][2], b1[2][2];
+    Bits b0[NB][2], b1[NB][2];
     load_b(b0, 0);
     __builtin_amdgcn_sched_barrier(0);
-    load_a(0, 0);
-    load_a(1, 1);
+#pragma unroll
+    for (int d = 0; d < Shape::kADist; ++d) load_a(d, d);
     __builtin_amdgcn_sched_barrier(0);
-    wait_vmcnt<kALoads>();         // B(0) and A(0) landed; A(1) in flight
+    wait_vmcnt<Shape::kALoads * (Shape::kADist - 1)>();   // B(0) and A(0) landed; later A in flight
     barrier_after_wait();
-    // One step: load B(st+1) into `next`, A(st+2); multiply B(st) held in
-    // `cur`; wait for A(st+1) and B(st+1); barrier.  The two B buffers swap
-    // roles by unrolling, so no register copy is needed.
-    auto step = [&](const Bits (&cur)[2][2], Bits (&next)[2][2], int st) {
+    // One step: load B(st+1) into `next`, A(st+Shape::kADist); multiply B(st) held
+    // in `cur`; wait for A(st+1) and B(st+1); barrier.  The two B buffers
+    // swap roles by unrolling, so no register copy is needed.
+    auto step = [&](const Bits (&cur)[NB][2], Bits (&next)[NB][2], int st) {
         load_b(next, st + 1);
         __builtin_amdgcn_sched_barrier(0);
-        load_a(st + 2, (st + 2) % kPStages);
+        load_a(st + Shape::kADist, (st + Shape::kADist) % Shape::kStages);
         __builtin_amdgcn_sched_barrier(0);
-        multiply(cur, st % kPStages);
+        multiply(cur, st % Shape::kStages);
         __builtin_amdgcn_sched_barrier(0);
-        wait_vmcnt<kALoads>();     // A(st+1) and B(st+1) landed; A(st+2) in flight
+        wait_vmcnt<Shape::kALoads * (Shape::kADist - 1)>();   // A(st+1) and B(st+1) landed
         barrier_after_wait();
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -975,48 +1004,62 @@ __global__ __launch_bounds__(256) void linear_prefill_kernel(
 
     // ---- epilogue ----
     // 32x32 block element e of lane l is D[8*(e/4) + 4*(l/32) + e%4][l%32].
-    // Each wave converts its 128 x 64 tile to fp16 (scale, rounding, bias)
-    // into its own LDS region, then writes it back row by row with 16-byte
-    // stores, eight lanes per 128-byte row segment.  The A stages are free by
-    // now; the clamped re-reads of the last steps must land before the
-    // region is reused.
+    // In passes of four row blocks (128 rows), each wave converts its part
+    // of the tile to fp16 (scale, rounding, bias) into its own LDS region,
+    // then writes it back row by row with 16-byte stores (4*NB lanes per
+    // row segment of 64*NB bytes).  The activation stages are free by now;
+    // the clamped re-reads of the last steps must land before the LDS is
+    // reused.
     wait_vmcnt<0>();
     __syncthreads();
-    constexpr int kCPitch = 144;                 // bytes per staged output row (128 + 16)
-    uint8_t* cw = xs + wave * (kPM * kCPitch);
-    const int nw0 = nb * kPN + wave * 64;        // first weight row of this wave
+    constexpr int kCols = 32 * NB;               // output columns per wave
+    constexpr int kCPitch = 2 * kCols + 16;      // bytes per staged output row
+    constexpr int kCRows = 128;                  // rows per pass
+    constexpr int kLanesPerRow = kCols / 8;      // 16-byte chunks per row
+    static_assert(4 * kCRows * kCPitch <= Shape::kLds, "output staging exceeds the activation LDS");
+    uint8_t* cw = xs + wave * (kCRows * kCPitch);
+    float sn[NB];
+    uint16_t bn[NB];
 #pragma unroll
-    for (int nb2 = 0; nb2 < 2; ++nb2) {
+    for (int nb2 = 0; nb2 < NB; ++nb2) {
         const int n = min(nw0 + 32 * nb2 + n32, m.rows - 1);
-        float sn = 1.0f;
-        if constexpr (MODE == kModeQ) sn = m.scales[n];
-        const uint16_t bn = bias ? bias[n] : uint16_t(0);
+        sn[nb2] = 1.0f;
+        bn[nb2] = 0;
+        if constexpr (MODE == kModeQ) sn[nb2] = m.scales[n];
+        if (bias) bn[nb2] = bias[n];
+    }
+    const bool yvec = (m.rows % 8 == 0) && (reinterpret_cast<uintptr_t>(y) % 16 == 0);
+    const int chunk = lane % kLanesPerRow;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+    for (int pass = 0; pass < MI / 4; ++pass) {
+        if (pass > 0) __syncthreads();
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int r = 32 * i + 8 * (e >> 2) + 4 * half + (e & 3);
-                *reinterpret_cast<uint16_t*>(cw + r * kCPitch + (32 * nb2 + n32) * 2) =
-                    epilogue<MODE>(acc[i][nb2][e], sn, bias != nullptr, bn);
+        for (int nb2 = 0; nb2 < NB; ++nb2) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int r = 32 * i + 8 * (e >> 2) + 4 * half + (e & 3);
+                    *reinterpret_cast<uint16_t*>(cw + r * kCPitch + (32 * nb2 + n32) * 2) =
+                        epilogue<MODE>(acc[4 * pass + i][nb2][e], sn[nb2], bias != nullptr, bn[nb2]);
+                }
             }
         }
-    }
-    __syncthreads();
-    const bool yvec = (m.rows % 8 == 0) && (reinterpret_cast<uintptr_t>(y) % 16 == 0);
-    const int chunk = lane & 7;
+        __syncthreads();
 #pragma unroll 4
-    for (int it = 0; it < kPM / 8; ++it) {
-        const int r = it * 8 + (lane >> 3);
-        const int gr = m0 + r;
-        const int gn = nw0 + chunk * 8;
-        if (gr >= M || gn >= m.rows) continue;
-        const uint4 v = *reinterpret_cast<const uint4*>(cw + r * kCPitch + chunk * 16);
-        uint16_t* dst = y + static_cast<size_t>(gr) * m.rows + gn;
-        if (yvec) {
-            *reinterpret_cast<uint4*>(dst) = v;
-        } else {
-            const uint16_t* h = reinterpret_cast<const uint16_t*>(&v);
-            for (int k = 0; k < 8 && gn + k < m.rows; ++k) dst[k] = h[k];
+        for (int it = 0; it < kCRows * kLanesPerRow / 64; ++it) {
+            const int r = it * (64 / kLanesPerRow) + lane / kLanesPerRow;
+            const int gr = m0 + pass * kCRows + r;
+            const int gn = nw0 + chunk * 8;
+            if (gr >= M || gn >= m.rows) continue;
+            const uint4 v = *reinterpret_cast<const uint4*>(cw + r * kCPitch + chunk * 16);
+            uint16_t* dst = y + static_cast<size_t>(gr) * m.rows + gn;
+            if (yvec) {
+                *reinterpret_cast<uint4*>(dst) = v;
+            } else {
+                const uint16_t* h = reinterpret_cast<const uint16_t*>(&v);
+                for (int k = 0; k < 8 && gn + k < m.rows; ++k) dst[k] = h[k];
+            }
         }
     }
 }
@@ -1095,6 +1138,19 @@ __global__ void packed_linear_kernel(const void* __restrict__ x, int x_dtype, in
 // dispatch helpers
 // ---------------------------------------------------------------------------
 
+// Compute units of the current device, cached per device.
+int device_cu_count() {
+    static int cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
 inline unsigned blocks_for(uint64_t n, unsigned threads) {
     return static_cast<unsigned>((n + threads - 1) / threads);
 }
@@ -1148,12 +1204,16 @@ struct MaterializeOp {
     }
 };
 
+#ifndef EBK_PREFILL_MI
+#define EBK_PREFILL_MI 4
+#endif
 #ifndef EBK_DECODE_WAVES
 #define EBK_DECODE_WAVES 8
 #endif
 #ifndef EBK_DECODE_GPL
 #define EBK_DECODE_GPL 1
 #endif
+constexpr int kPrefillMI = EBK_PREFILL_MI;
 constexpr int kDecodeWaves = EBK_DECODE_WAVES;
 constexpr int kDecodeGpl = EBK_DECODE_GPL;
 constexpr int kDecodeMaxM = 16;
@@ -1172,11 +1232,31 @@ hipError_t run_linear_mode(const DevMatrix& m, const uint16_t* x, int64_t M, uin
         }
     } else if (MODE != kModeRaw && xvec && static_cast<uint64_t>(M) * m.cols * 2 < (uint64_t(1) << 32)) {
         if constexpr (MODE != kModeRaw) {
-            const int mblocks = static_cast<int>((M + kPM - 1) / kPM);
+            // Full tiles are 128 x 256.  When the last round of full tiles
+            // would leave at least half the CUs idle, its tiles run as two
+            // 128 x 128 halves instead, so it takes half a round.
+            constexpr int kRows = 32 * kPrefillMI;
+            const int mblocks = static_cast<int>((M + kRows - 1) / kRows);
             const int nblocks = (m.rows + kPN - 1) / kPN;
-            const int per_xcd = (mblocks * nblocks + 7) / 8;
-            hipLaunchKernelGGL((linear_prefill_kernel<B, MODE>), dim3(8 * per_xcd), dim3(256), 0, s, m, x,
-                               static_cast<int>(M), y, bias, mblocks, nblocks, per_xcd);
+            const int tiles = mblocks * nblocks;
+            const int cus = device_cu_count();
+            int full = tiles;
+            if (tiles <= cus / 2) {
+                full = 0;
+            } else if (tiles % cus != 0 && tiles % cus <= cus / 2) {
+                full = tiles - tiles % cus;
+            }
+            if (full > 0) {
+                const int per_xcd = (full + 7) / 8;
+                hipLaunchKernelGGL((linear_prefill_kernel<B, MODE, kPrefillMI, 2>), dim3(8 * per_xcd), dim3(256), 0,
+                                   s, m, x, static_cast<int>(M), y, bias, mblocks, nblocks, 0, full, per_xcd);
+            }
+            if (full < tiles) {
+                const int jobs = 2 * (tiles - full);
+                const int per_xcd = (jobs + 7) / 8;
+                hipLaunchKernelGGL((linear_prefill_kernel<B, MODE, kPrefillMI, 1>), dim3(8 * per_xcd), dim3(256), 0,
+                                   s, m, x, static_cast<int>(M), y, bias, mblocks, nblocks, full, jobs, per_xcd);
+            }
         }
     } else {
         const dim3 grid((m.rows + kBN - 1) / kBN, static_cast<unsigned>((M + kBM - 1) / kBM));
