@@ -820,8 +820,8 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <int B, int MODE, int MI, int NB>
-__global__ __launch_bounds__(256) void linear_prefill_kernel(
+template <int B, int MODE, int MI, int NB, int KS>
+__global__ __launch_bounds__(256 * KS) void linear_prefill_kernel(
     DevMatrix m, const uint16_t* __restrict__ x, int M, uint16_t* __restrict__ y,
     const uint16_t* __restrict__ bias, int mblocks, int nblocks, int tile0, int njobs, int per_xcd) {
     static_assert(MODE != kModeRaw, "raw fp16 weights use linear_gemm_kernel");
@@ -830,6 +830,8 @@ __global__ __launch_bounds__(256) void linear_prefill_kernel(
     __shared__ __attribute__((aligned(16))) uint8_t xs[Shape::kLds];
 
     static_assert(NB == 1 || NB == 2, "32 or 64 weight rows per wave");
+    static_assert(KS == 1 || KS == 2, "one or two waves per weight column group");
+    constexpr int kPL = 2 / KS;                     // group pairs (of a step's 4 groups) per wave
     // ---- tile of this workgroup (uniform early exit, before any barrier) ----
     // Jobs j = 0 .. njobs-1 cover the full tiles tile0, tile0+1, ... of the
     // grouped order (128 x 256); with NB = 1 two jobs split a full tile into
@@ -849,7 +851,9 @@ __global__ __launch_bounds__(256) void linear_prefill_kernel(
     const int n0 = nb * kPN + (NB == 2 ? 0 : (job & 1) * (kPN / 2));
 
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wave_id = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // 0 .. 4*KS-1
+    const int wave = wave_id & 3;                   // weight column group
+    const int kp = wave_id >> 2;                    // K half of each step (KS = 2)
     const int n32 = lane & 31;
     const int half = lane >> 5;
     const int steps = m.spr;
@@ -858,16 +862,17 @@ __global__ __launch_bounds__(256) void linear_prefill_kernel(
     // B slots of this lane: [nb2][p] -> row tile 2*nb2 + n32/16 of the wave,
     // slot 16*(2p + half) + n32%16 (row tiles clamped; rows past the end are
     // never stored).  Slot indices fit 32 bits (planes below 4 GiB).
-    uint32_t slot0[NB][2];
+    uint32_t slot0[NB][kPL];
     float s[NB];
 #pragma unroll
     for (int nb2 = 0; nb2 < NB; ++nb2) {
         s[nb2] = 0.0f;
         const int rt = min(nw0 / kTileRows + 2 * nb2 + (n32 >> 4), m.rtiles - 1);
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            slot0[nb2][p] = static_cast<uint32_t>(rt) * static_cast<uint32_t>(steps * kTileSlots) +
-                            static_cast<uint32_t>(16 * (2 * p + half) + (n32 & 15));
+        for (int pl = 0; pl < kPL; ++pl) {
+            const int p = KS == 2 ? kp : pl;
+            slot0[nb2][pl] = static_cast<uint32_t>(rt) * static_cast<uint32_t>(steps * kTileSlots) +
+                             static_cast<uint32_t>(16 * (2 * p + half) + (n32 & 15));
         }
         if constexpr (MODE == kModeW) {
             const int row = rt * kTileRows + (n32 & 15);
@@ -887,27 +892,29 @@ __global__ __launch_bounds__(256) void linear_prefill_kernel(
     int achunk[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) achunk[i] = 8 * ((lane & 15) ^ ((4 * i + (lane >> 4)) & 15));
-    const int arow0 = m0 + wave * (Shape::kRows / 4) + (lane >> 4);
+    constexpr int kAWaveRows = Shape::kRows / (4 * KS);   // rows each wave loads
+    constexpr int kAWaveLoads = kAWaveRows / 4;          // 1 KB instructions per wave
+    const int arow0 = m0 + wave_id * kAWaveRows + (lane >> 4);
     const uint8_t* xb = reinterpret_cast<const uint8_t*>(x);
     auto load_a = [&](int st, int stage) {
         const int k0 = min(st, steps - 1) * kPK;
         const int kmax = m.cols - 8;
 #pragma unroll
-        for (int i = 0; i < Shape::kALoads; ++i) {
+        for (int i = 0; i < kAWaveLoads; ++i) {
             const uint32_t row = static_cast<uint32_t>(min(arow0 + 4 * i, M - 1));
             const uint32_t off = 2u * (row * static_cast<uint32_t>(m.cols) +
                                        static_cast<uint32_t>(min(k0 + achunk[i & 3], kmax)));
             __builtin_amdgcn_global_load_lds(xb + off, (lds_void_ptr)(xs + stage * Shape::kStage +
-                                                                      (wave * (Shape::kRows / 4) + i * 4) * kPRow),
+                                                                      (wave_id * kAWaveRows + i * 4) * kPRow),
                                              16, 0, 0);
         }
     };
-    auto load_b = [&](Bits (&bits)[NB][2], int st) {
+    auto load_b = [&](Bits (&bits)[NB][kPL], int st) {
         const uint32_t off = static_cast<uint32_t>(min(st, steps - 1) * kTileSlots);
 #pragma unroll
         for (int nb2 = 0; nb2 < NB; ++nb2)
 #pragma unroll
-            for (int p = 0; p < 2; ++p) bits[nb2][p].load32(m, slot0[nb2][p] + off);
+            for (int pl = 0; pl < kPL; ++pl) bits[nb2][pl].load32(m, slot0[nb2][pl] + off);
     };
 
     floatx16 acc[MI][NB];
@@ -932,9 +939,9 @@ __global__ __launch_bounds__(256) void linear_prefill_kernel(
     // slice pt run, then wait for the reads.  sched_barrier pins the slice
     // boundaries; inside a slice the compiler interleaves the decode VALU
     // with the MFMAs.
-    auto decode_pt = [&](const Bits (&cur)[NB][2], half8 (&bop)[NB], int pt) {
+    auto decode_pt = [&](const Bits (&cur)[NB][kPL], half8 (&bop)[NB], int ps) {
 #pragma unroll
-        for (int nb2 = 0; nb2 < NB; ++nb2) bop[nb2] = cur[nb2][pt >> 2].operand(pt & 3, s[nb2]);
+        for (int nb2 = 0; nb2 < NB; ++nb2) bop[nb2] = cur[nb2][ps >> 2].operand(ps & 3, s[nb2]);
     };
     auto mfma_pt = [&](const half8 (&a)[MI], const half8 (&bop)[NB]) {
 #pragma unroll
@@ -945,22 +952,25 @@ __global__ __launch_bounds__(256) void linear_prefill_kernel(
             }
         }
     };
-    auto multiply = [&](const Bits (&cur)[NB][2], int stage) {
+    // Local slice ps covers group pair (KS == 2 ? kp : ps/4), codes t = ps%4.
+    auto pair_of = [&](int ps) { return KS == 2 ? kp : (ps >> 2); };
+    auto multiply = [&](const Bits (&cur)[NB][kPL], int stage) {
+        constexpr int kSlices = 4 * kPL;
         half8 a0[MI], a1[MI];
         half8 b0[NB], b1[NB];
-        read_a(a0, stage, 0, 0);
+        read_a(a0, stage, pair_of(0), 0);
         decode_pt(cur, b0, 0);
         wait_lgkmcnt<0>();
 #pragma unroll
-        for (int pt = 0; pt < 8; pt += 2) {
-            read_a(a1, stage, (pt + 1) >> 2, (pt + 1) & 3);
-            decode_pt(cur, b1, pt + 1);
+        for (int ps = 0; ps < kSlices; ps += 2) {
+            read_a(a1, stage, pair_of(ps + 1), (ps + 1) & 3);
+            decode_pt(cur, b1, ps + 1);
             mfma_pt(a0, b0);
             __builtin_amdgcn_sched_barrier(0);
             wait_lgkmcnt<0>();
-            if (pt + 2 < 8) {
-                read_a(a0, stage, (pt + 2) >> 2, (pt + 2) & 3);
-                decode_pt(cur, b0, pt + 2);
+            if (ps + 2 < kSlices) {
+                read_a(a0, stage, pair_of(ps + 2), (ps + 2) & 3);
+                decode_pt(cur, b0, ps + 2);
             }
             mfma_pt(a1, b1);
             __builtin_amdgcn_sched_barrier(0);
@@ -973,25 +983,25 @@ __global__ __launch_bounds__(256) void linear_prefill_kernel(
     // everything except the A batch just issued, i.e. for A(st+1) and
     // B(st+1).  sched_barrier keeps the compiler from sinking the loads into
     // the multiply.
-    Bits b0[NB][2], b1[NB][2];
+    Bits b0[NB][kPL], b1[NB][kPL];
     load_b(b0, 0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int d = 0; d < Shape::kADist; ++d) load_a(d, d);
     __builtin_amdgcn_sched_barrier(0);
-    wait_vmcnt<Shape::kALoads * (Shape::kADist - 1)>();   // B(0) and A(0) landed; later A in flight
+    wait_vmcnt<kAWaveLoads * (Shape::kADist - 1)>();   // B(0) and A(0) landed; later A in flight
     barrier_after_wait();
     // One step: load B(st+1) into `next`, A(st+Shape::kADist); multiply B(st) held
     // in `cur`; wait for A(st+1) and B(st+1); barrier.  The two B buffers
     // swap roles by unrolling, so no register copy is needed.
-    auto step = [&](const Bits (&cur)[NB][2], Bits (&next)[NB][2], int st) {
+    auto step = [&](const Bits (&cur)[NB][kPL], Bits (&next)[NB][kPL], int st) {
         load_b(next, st + 1);
         __builtin_amdgcn_sched_barrier(0);
         load_a(st + Shape::kADist, (st + Shape::kADist) % Shape::kStages);
         __builtin_amdgcn_sched_barrier(0);
         multiply(cur, st % Shape::kStages);
         __builtin_amdgcn_sched_barrier(0);
-        wait_vmcnt<Shape::kALoads * (Shape::kADist - 1)>();   // A(st+1) and B(st+1) landed
+        wait_vmcnt<kAWaveLoads * (Shape::kADist - 1)>();   // A(st+1) and B(st+1) landed
         barrier_after_wait();
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -1012,6 +1022,32 @@ __global__ __launch_bounds__(256) void linear_prefill_kernel(
     // reused.
     wait_vmcnt<0>();
     __syncthreads();
+    if constexpr (KS == 2) {
+        // The K-half-1 waves hand their partial sums to the K-half-0 waves
+        // of the same column group through LDS, two row blocks at a time.
+        float* red = reinterpret_cast<float*>(xs) + wave * (2 * NB * 16 * 64);
+#pragma unroll
+        for (int h = 0; h < MI / 2; ++h) {
+            if (kp == 1) {
+#pragma unroll
+                for (int i2 = 0; i2 < 2; ++i2)
+#pragma unroll
+                    for (int nb2 = 0; nb2 < NB; ++nb2)
+#pragma unroll
+                        for (int e = 0; e < 16; ++e) red[((i2 * NB + nb2) * 16 + e) * 64 + lane] = acc[2 * h + i2][nb2][e];
+            }
+            __syncthreads();
+            if (kp == 0) {
+#pragma unroll
+                for (int i2 = 0; i2 < 2; ++i2)
+#pragma unroll
+                    for (int nb2 = 0; nb2 < NB; ++nb2)
+#pragma unroll
+                        for (int e = 0; e < 16; ++e) acc[2 * h + i2][nb2][e] += red[((i2 * NB + nb2) * 16 + e) * 64 + lane];
+            }
+            __syncthreads();
+        }
+    }
     constexpr int kCols = 32 * NB;               // output columns per wave
     constexpr int kCPitch = 2 * kCols + 16;      // bytes per staged output row
     constexpr int kCRows = 128;                  // rows per pass
@@ -1033,6 +1069,7 @@ __global__ __launch_bounds__(256) void linear_prefill_kernel(
 #pragma unroll
     for (int pass = 0; pass < MI / 4; ++pass) {
         if (pass > 0) __syncthreads();
+        if (kp == 0) {
 #pragma unroll
         for (int nb2 = 0; nb2 < NB; ++nb2) {
 #pragma unroll
@@ -1045,7 +1082,9 @@ __global__ __launch_bounds__(256) void linear_prefill_kernel(
                 }
             }
         }
+        }
         __syncthreads();
+        if (kp != 0) continue;
 #pragma unroll 4
         for (int it = 0; it < kCRows * kLanesPerRow / 64; ++it) {
             const int r = it * (64 / kLanesPerRow) + lane / kLanesPerRow;
@@ -1204,6 +1243,9 @@ struct MaterializeOp {
     }
 };
 
+#ifndef EBK_PREFILL_KS
+#define EBK_PREFILL_KS 2
+#endif
 #ifndef EBK_PREFILL_MI
 #define EBK_PREFILL_MI 4
 #endif
@@ -1214,6 +1256,7 @@ struct MaterializeOp {
 #define EBK_DECODE_GPL 1
 #endif
 constexpr int kPrefillMI = EBK_PREFILL_MI;
+constexpr int kPrefillKS = EBK_PREFILL_KS;
 constexpr int kDecodeWaves = EBK_DECODE_WAVES;
 constexpr int kDecodeGpl = EBK_DECODE_GPL;
 constexpr int kDecodeMaxM = 16;
@@ -1248,14 +1291,16 @@ hipError_t run_linear_mode(const DevMatrix& m, const uint16_t* x, int64_t M, uin
             }
             if (full > 0) {
                 const int per_xcd = (full + 7) / 8;
-                hipLaunchKernelGGL((linear_prefill_kernel<B, MODE, kPrefillMI, 2>), dim3(8 * per_xcd), dim3(256), 0,
-                                   s, m, x, static_cast<int>(M), y, bias, mblocks, nblocks, 0, full, per_xcd);
+                hipLaunchKernelGGL((linear_prefill_kernel<B, MODE, kPrefillMI, 2, kPrefillKS>), dim3(8 * per_xcd),
+                                   dim3(256 * kPrefillKS), 0, s, m, x, static_cast<int>(M), y, bias, mblocks, nblocks, 0,
+                                   full, per_xcd);
             }
             if (full < tiles) {
                 const int jobs = 2 * (tiles - full);
                 const int per_xcd = (jobs + 7) / 8;
-                hipLaunchKernelGGL((linear_prefill_kernel<B, MODE, kPrefillMI, 1>), dim3(8 * per_xcd), dim3(256), 0,
-                                   s, m, x, static_cast<int>(M), y, bias, mblocks, nblocks, full, jobs, per_xcd);
+                hipLaunchKernelGGL((linear_prefill_kernel<B, MODE, kPrefillMI, 1, kPrefillKS>), dim3(8 * per_xcd),
+                                   dim3(256 * kPrefillKS), 0, s, m, x, static_cast<int>(M), y, bias, mblocks, nblocks,
+                                   full, jobs, per_xcd);
             }
         }
     } else {
