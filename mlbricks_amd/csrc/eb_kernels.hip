@@ -1015,11 +1015,11 @@ __global__ __launch_bounds__(256 * KS) void linear_prefill_kernel(
     // ---- epilogue ----
     // 32x32 block element e of lane l is D[8*(e/4) + 4*(l/32) + e%4][l%32].
     // In passes of four row blocks (128 rows), each wave converts its part
-    // of the tile to fp16 (scale, rounding, bias) into its own LDS region,
-    // then writes it back row by row with 16-byte stores (4*NB lanes per
-    // row segment of 64*NB bytes).  The activation stages are free by now;
-    // the clamped re-reads of the last steps must land before the LDS is
-    // reused.
+    // of the tile to fp16 (scale, rounding, bias) into the workgroup's LDS
+    // copy of the tile, then all waves write it back row by row with
+    // 16-byte stores, each row one contiguous segment.  The activation
+    // stages are free by now; the clamped re-reads of the last steps must
+    // land before the LDS is reused.
     wait_vmcnt<0>();
     __syncthreads();
     if constexpr (KS == 2) {
@@ -1049,11 +1049,12 @@ __global__ __launch_bounds__(256 * KS) void linear_prefill_kernel(
         }
     }
     constexpr int kCols = 32 * NB;               // output columns per wave
-    constexpr int kCPitch = 2 * kCols + 16;      // bytes per staged output row
+    constexpr int kTileCols = 4 * kCols;         // output columns per workgroup
+    constexpr int kCPitch = 2 * kTileCols + 16;  // bytes per staged output row
     constexpr int kCRows = 128;                  // rows per pass
-    constexpr int kLanesPerRow = kCols / 8;      // 16-byte chunks per row
-    static_assert(4 * kCRows * kCPitch <= Shape::kLds, "output staging exceeds the activation LDS");
-    uint8_t* cw = xs + wave * (kCRows * kCPitch);
+    constexpr int kLanesPerRow = kTileCols / 8;  // 16-byte chunks per row
+    constexpr int kThreads = 256 * KS;
+    static_assert(kCRows * kCPitch <= Shape::kLds, "output staging exceeds the activation LDS");
     float sn[NB];
     uint16_t bn[NB];
 #pragma unroll
@@ -1065,33 +1066,35 @@ __global__ __launch_bounds__(256 * KS) void linear_prefill_kernel(
         if (bias) bn[nb2] = bias[n];
     }
     const bool yvec = (m.rows % 8 == 0) && (reinterpret_cast<uintptr_t>(y) % 16 == 0);
-    const int chunk = lane % kLanesPerRow;
+    const int chunk = threadIdx.x % kLanesPerRow;
 #pragma unroll
     for (int pass = 0; pass < MI / 4; ++pass) {
         if (pass > 0) __syncthreads();
+        // the whole workgroup tile goes to LDS so that rows leave as
+        // contiguous 2*kTileCols-byte segments
         if (kp == 0) {
+            uint8_t* cw = xs + wave * kCols * 2;
 #pragma unroll
-        for (int nb2 = 0; nb2 < NB; ++nb2) {
+            for (int nb2 = 0; nb2 < NB; ++nb2) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+                for (int i = 0; i < 4; ++i) {
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int r = 32 * i + 8 * (e >> 2) + 4 * half + (e & 3);
-                    *reinterpret_cast<uint16_t*>(cw + r * kCPitch + (32 * nb2 + n32) * 2) =
-                        epilogue<MODE>(acc[4 * pass + i][nb2][e], sn[nb2], bias != nullptr, bn[nb2]);
+                    for (int e = 0; e < 16; ++e) {
+                        const int r = 32 * i + 8 * (e >> 2) + 4 * half + (e & 3);
+                        *reinterpret_cast<uint16_t*>(cw + r * kCPitch + (32 * nb2 + n32) * 2) =
+                            epilogue<MODE>(acc[4 * pass + i][nb2][e], sn[nb2], bias != nullptr, bn[nb2]);
+                    }
                 }
             }
         }
-        }
         __syncthreads();
-        if (kp != 0) continue;
-#pragma unroll 4
-        for (int it = 0; it < kCRows * kLanesPerRow / 64; ++it) {
-            const int r = it * (64 / kLanesPerRow) + lane / kLanesPerRow;
+#pragma unroll 2
+        for (int it = 0; it < kCRows * kLanesPerRow / kThreads; ++it) {
+            const int r = it * (kThreads / kLanesPerRow) + static_cast<int>(threadIdx.x) / kLanesPerRow;
             const int gr = m0 + pass * kCRows + r;
-            const int gn = nw0 + chunk * 8;
+            const int gn = n0 + chunk * 8;
             if (gr >= M || gn >= m.rows) continue;
-            const uint4 v = *reinterpret_cast<const uint4*>(cw + r * kCPitch + chunk * 16);
+            const uint4 v = *reinterpret_cast<const uint4*>(xs + r * kCPitch + chunk * 16);
             uint16_t* dst = y + static_cast<size_t>(gr) * m.rows + gn;
             if (yvec) {
                 *reinterpret_cast<uint4*>(dst) = v;
