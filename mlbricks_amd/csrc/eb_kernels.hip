@@ -781,6 +781,12 @@ constexpr int kPGroupM = 4;                // activation blocks per tile-order g
 // the cast has the same effect).
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
 
+// Vector-memory instructions one GroupBits::load32 issues (kModeQ / kModeW).
+template <int B>
+constexpr int group_loads() {
+    return (Planes<B>::h8 ? 2 : 0) + (Planes<B>::h4 ? 1 : 0) + (Planes<B>::h2 ? 1 : 0) + (Planes<B>::h1 ? 1 : 0);
+}
+
 // Prefill tile geometry for MI 32-row activation blocks per wave.
 template <int MI>
 struct PrefillShape {
@@ -979,37 +985,57 @@ __global__ __launch_bounds__(256 * KS) void linear_prefill_kernel(
     };
 
     // Issue order matters (vector loads retire in order).  Per step: B of
-    // step st+1, then A of step st+2.  Before the barrier the wave waits for
-    // everything except the A batch just issued, i.e. for A(st+1) and
-    // B(st+1).  sched_barrier keeps the compiler from sinking the loads into
-    // the multiply.
-    Bits b0[NB][kPL], b1[NB][kPL];
-    load_b(b0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int d = 0; d < Shape::kADist; ++d) load_a(d, d);
-    __builtin_amdgcn_sched_barrier(0);
-    wait_vmcnt<kAWaveLoads * (Shape::kADist - 1)>();   // B(0) and A(0) landed; later A in flight
-    barrier_after_wait();
-    // One step: load B(st+1) into `next`, A(st+Shape::kADist); multiply B(st) held
-    // in `cur`; wait for A(st+1) and B(st+1); barrier.  The two B buffers
-    // swap roles by unrolling, so no register copy is needed.
+    // step st+kBDist, then A of step st+kADist.  Before the barrier the wave
+    // waits for everything except the batches just issued, i.e. for A(st+1)
+    // and B(st+1).  sched_barrier keeps the compiler from sinking the loads
+    // into the multiply.  With two waves per column group and codes of at
+    // most 10 bits the register budget holds a third B buffer, so B is
+    // prefetched two steps ahead; the buffers rotate by unrolling, so no
+    // register copy is needed.
+    constexpr int kBDist = (KS == 2 && B <= 10) ? 2 : 1;
+    constexpr int kBLoads = NB * kPL * group_loads<B>();   // B loads per step per wave
     auto step = [&](const Bits (&cur)[NB][kPL], Bits (&next)[NB][kPL], int st) {
-        load_b(next, st + 1);
+        load_b(next, st + kBDist);
         __builtin_amdgcn_sched_barrier(0);
         load_a(st + Shape::kADist, (st + Shape::kADist) % Shape::kStages);
         __builtin_amdgcn_sched_barrier(0);
         multiply(cur, st % Shape::kStages);
         __builtin_amdgcn_sched_barrier(0);
-        wait_vmcnt<kAWaveLoads * (Shape::kADist - 1)>();   // A(st+1) and B(st+1) landed
+        // A(st+1) and B(st+1) landed
+        wait_vmcnt<kAWaveLoads * (Shape::kADist - 1) + kBLoads * (kBDist - 1)>();
         barrier_after_wait();
         __builtin_amdgcn_sched_barrier(0);
     };
-    for (int st = 0;; st += 2) {
-        step(b0, b1, st);
-        if (st + 1 >= steps) break;
-        step(b1, b0, st + 1);
-        if (st + 2 >= steps) break;
+    Bits b0[NB][kPL], b1[NB][kPL], b2[NB][kPL];
+    load_b(b0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    load_a(0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kBDist == 2) load_b(b1, 1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int d = 1; d < Shape::kADist; ++d) load_a(d, d);
+    __builtin_amdgcn_sched_barrier(0);
+    // B(0) and A(0) landed; the later batches may be in flight
+    wait_vmcnt<kAWaveLoads * (Shape::kADist - 1) + kBLoads * (kBDist - 1)>();
+    barrier_after_wait();
+    if constexpr (kBDist == 2) {
+        for (int st = 0;; st += 3) {
+            step(b0, b2, st);
+            if (st + 1 >= steps) break;
+            step(b1, b0, st + 1);
+            if (st + 2 >= steps) break;
+            step(b2, b1, st + 2);
+            if (st + 3 >= steps) break;
+        }
+    } else {
+        (void)b2;
+        for (int st = 0;; st += 2) {
+            step(b0, b1, st);
+            if (st + 1 >= steps) break;
+            step(b1, b0, st + 1);
+            if (st + 2 >= steps) break;
+        }
     }
 
     // ---- epilogue ----

@@ -296,3 +296,34 @@ def test_legacy_packed_linear_dtypes_and_torch_op(native, dtype):
                             bias.double().cpu().numpy(), b, G, N, K).reshape(2, 3, N)
     tol = 1e-5 if dtype == torch.float32 else 1e-2
     assert _rel_max(y.double().cpu().numpy(), ref) <= tol
+
+
+# Prefill tiling: the launcher runs whole 128 x 256 tiles, splits a partial
+# last round into 128 x 128 halves, and covers ragged M, N and K (columns
+# past K meet zero-padded codes; rows past M or N are never stored).  These
+# shapes hit: only half tiles (108 tiles), only whole tiles (204), and a mix
+# (308 = 256 whole + 52 split), each with a partial K step, in both the
+# integer-dot and the decoded-fp16 arithmetic.
+@pytest.mark.parametrize("rows,cols,M,b,policy", [
+    (3000, 1000, 1100, 7, "hardwareNative"),
+    (2900, 1000, 2100, 10, "hardwareNative"),
+    (7000, 520, 1300, 12, "hardwareNative"),
+    (7000, 520, 1300, 9, "fullPrecision"),
+])
+def test_prefill_tiling_shapes_match_decoded_product(native, rows, cols, M, b, policy):
+    rng = np.random.default_rng(rows + cols + M + b)
+    q = _codes(rng, rows, cols, b)
+    s = rng.uniform(0.002, 0.05, size=rows).astype(np.float32)
+    m = native.RuntimeMatrix._compressSelectedCodes(q, s, b, 0.01, 0.0, policy)
+    x = torch.from_numpy(rng.standard_normal((M, cols)).astype(np.float16)).cuda()
+    y = m.forwardTorch(x)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y).all()
+    wd = m._materializeTorch().float()
+    full = torch.matmul(x.float(), wd.T.contiguous())
+    assert float((y.float() - full).abs().max() / full.abs().max()) <= TOL
+    # a row/column corner against the fp64 oracle of the reference formula
+    sub_r, sub_m = 32, 64
+    payload = ora.pack_codes(q[:sub_r], b)
+    ref = _reference(payload, s[:sub_r], sub_r, cols, b, x[-sub_m:].cpu().numpy().view(np.uint16), policy)
+    assert _rel_max(y[-sub_m:, :sub_r].float().cpu().numpy(), ref) <= TOL
