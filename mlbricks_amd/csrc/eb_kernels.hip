@@ -363,6 +363,38 @@ __device__ __forceinline__ void load_x32(const uint16_t* __restrict__ xrow, int 
     }
 }
 
+// An LDS address as the address-space-3 pointer global_load_lds takes.  The
+// explicit cast at the call matters: without it hipcc's host pass silently
+// drops the launch stub of a kernel template that passes an LDS array
+// expression of dependent type to the builtin (and a __device__ helper doing
+// the cast has the same effect).
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+
+// Workgroup barrier for the direct-to-LDS pipeline.  __syncthreads() opens
+// with a release fence, which waits for every outstanding vector load --
+// including the prefetch that should stay in flight across the barrier.
+// The caller waits for the loads the next step reads (wait_vmcnt) and the
+// barrier keeps only the acquire side.  Prior LDS reads have all returned:
+// their MFMAs consumed them.
+__device__ __forceinline__ void barrier_after_wait() {
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// s_waitcnt with only the LDS / scalar-memory counter constrained.
+template <int N>
+__device__ __forceinline__ void wait_lgkmcnt() {
+    static_assert(N >= 0 && N < 16, "lgkmcnt is a 4-bit counter");
+    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4) | (N << 8));
+}
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 // ---------------------------------------------------------------------------
 // decode kernel, M <= 16: one workgroup owns one row tile (16 weight rows);
 // its WAVES waves split the row tile's K tiles.  In step `st` lane l loads
@@ -405,6 +437,15 @@ struct GroupBits<B, kModeRaw> {
         for (int t = 0; t < 4; ++t) w[t] = p[t];
     }
     __device__ __forceinline__ half8 operand(int t, float) const { return __builtin_bit_cast(half8, w[t]); }
+};
+
+// Vector-memory instructions one GroupBits::load issues.
+template <int B, int MODE>
+struct GroupLoads {
+    static constexpr int value =
+        MODE == kModeRaw ? 4
+                         : (Planes<B>::h8 ? 2 : 0) + (Planes<B>::h4 ? 1 : 0) + (Planes<B>::h2 ? 1 : 0) +
+                               (Planes<B>::h1 ? 1 : 0);
 };
 
 // Eight activations x[r][k .. k+8) as one uint4, zero at and beyond `cols`.
@@ -511,14 +552,30 @@ __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
 
     uint4 xv[XLDS ? kXVecs : 1];
     const int vpr = kpad / 8;                        // uint4 vectors per staged row
+    // xvec == 2: rows are whole tiles wide (cols == kpad) and x is 16-byte
+    // aligned, so the staged copy is x itself and goes global -> LDS
+    // directly, without registers; otherwise through registers, zero-padded.
+    const bool xdirect = xvec == 2;
     if constexpr (XLDS) {
+        if (xdirect) {
 #pragma unroll
-        for (int r = 0; r < kXVecs; ++r) {
-            const int i = threadIdx.x + r * kThreads;
-            xv[r] = make_uint4(0, 0, 0, 0);
-            if (i < M * vpr) {
-                const int mi = i / vpr;
-                xv[r] = load_x8(x, mi, (i - mi * vpr) * 8, m.cols, xvec != 0);
+            for (int r = 0; r < kXVecs; ++r) {
+                const int i = threadIdx.x + r * kThreads;
+                if (i < M * vpr) {
+                    __builtin_amdgcn_global_load_lds(x + 8 * i,
+                                                     (lds_void_ptr)(xs + 8 * (r * kThreads + (threadIdx.x & ~63))),
+                                                     16, 0, 0);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < kXVecs; ++r) {
+                const int i = threadIdx.x + r * kThreads;
+                xv[r] = make_uint4(0, 0, 0, 0);
+                if (i < M * vpr) {
+                    const int mi = i / vpr;
+                    xv[r] = load_x8(x, mi, (i - mi * vpr) * 8, m.cols, xvec != 0);
+                }
             }
         }
     }
@@ -543,12 +600,18 @@ __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
     // flight, which already covers the loaded HBM latency.
     decode_load_batch<GPL>(m, buf0, slot0, wave * GPL, steps);
     if constexpr (XLDS) {
+        if (xdirect) {
+            // the activation loads precede the weight loads just issued
+            wait_vmcnt<GPL * GroupLoads<B, MODE>::value>();
+            barrier_after_wait();
+        } else {
 #pragma unroll
-        for (int r = 0; r < kXVecs; ++r) {
-            const int i = threadIdx.x + r * kThreads;
-            if (i < M * vpr) *reinterpret_cast<uint4*>(xs + 8 * i) = xv[r];
+            for (int r = 0; r < kXVecs; ++r) {
+                const int i = threadIdx.x + r * kThreads;
+                if (i < M * vpr) *reinterpret_cast<uint4*>(xs + 8 * i) = xv[r];
+            }
+            __syncthreads();
         }
-        __syncthreads();
     }
     auto batch = [&](const Bits (&cur)[GPL], Bits (&nxt)[GPL], bool prefetch, int bi) {
         decode_activations<GPL, XLDS>(a, m, bi * kBatch, wave, quarter, m_ok, steps, xrow, xsrow, xvec);
@@ -774,13 +837,6 @@ constexpr int kPK = kTileGroups * kGroup;  // 128 columns per step
 constexpr int kPRow = kPK * 2;             // bytes per staged activation row
 constexpr int kPGroupM = 4;                // activation blocks per tile-order group
 
-// An LDS address as the address-space-3 pointer global_load_lds takes.  The
-// explicit cast at the call matters: without it hipcc's host pass silently
-// drops the launch stub of a kernel template that passes an LDS array
-// expression of dependent type to the builtin (and a __device__ helper doing
-// the cast has the same effect).
-typedef __attribute__((address_space(3))) void* lds_void_ptr;
-
 // Vector-memory instructions one GroupBits::load32 issues (kModeQ / kModeW).
 template <int B>
 constexpr int group_loads() {
@@ -800,31 +856,6 @@ struct PrefillShape {
     static constexpr int kALoads = kRows / 16;       // A loads per step per wave (1 KB each)
     static constexpr int kADist = kStages - 1;       // activation prefetch distance
 };
-
-// Workgroup barrier for the direct-to-LDS pipeline.  __syncthreads() opens
-// with a release fence, which waits for every outstanding vector load --
-// including the prefetch that should stay in flight across the barrier.
-// The caller waits for the loads the next step reads (wait_vmcnt) and the
-// barrier keeps only the acquire side.  Prior LDS reads have all returned:
-// their MFMAs consumed them.
-__device__ __forceinline__ void barrier_after_wait() {
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-}
-
-// s_waitcnt with only the LDS / scalar-memory counter constrained.
-template <int N>
-__device__ __forceinline__ void wait_lgkmcnt() {
-    static_assert(N >= 0 && N < 16, "lgkmcnt is a 4-bit counter");
-    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4) | (N << 8));
-}
-
-// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 
 template <int B, int MODE, int MI, int NB, int KS>
 __global__ __launch_bounds__(256 * KS) void linear_prefill_kernel(
@@ -1379,7 +1410,10 @@ hipError_t launch_materialize(const DevMatrix& m, uint16_t* out, hipStream_t str
 
 hipError_t launch_linear(const DevMatrix& m, bool exact_w16, const uint16_t* x, int64_t M, uint16_t* y,
                          const uint16_t* bias, hipStream_t stream) {
-    const int xvec = (m.cols % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0);
+    // 1: rows of x can be read 16 bytes at a time; 2: and they span whole
+    // 128-column tiles, so x needs no zero padding
+    int xvec = (m.cols % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0);
+    if (xvec && m.cols % (kTileGroups * kGroup) == 0) xvec = 2;
     if (m.bits == 16) return run_linear_mode<8, kModeRaw>(m, x, M, y, bias, xvec, stream);
     return dispatch_bits<LinearOp>(m.bits, m, exact_w16, x, M, y, bias, xvec, stream);
 }
