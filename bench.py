@@ -13,6 +13,12 @@ bytes counted at the storage width: ceil(N*K*b/8) + 4N + 2MK + 2MN.
 
 Also reported (not the headline): the prefill GEMM of configs[3] (4096->14336,
 M=2048) in TFLOP/s, and the oracle's OpenMP CPU GEMV on the host's cores.
+
+Profiling helpers (same file, so the committed summaries name committed code):
+
+    python bench.py --traffic-probe      # eager launches for rocprofv3 --pmc passes
+    python bench.py --summarize-pmc FETCH.csv WRITE.csv    # -> profiles/*_traffic.md
+    python bench.py --summarize-trace KERNEL_STATS.csv     # -> kernel table (markdown)
 """
 from __future__ import annotations
 
@@ -31,6 +37,13 @@ if str(ROOT) not in sys.path:
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 FP16_PEAK_TFLOPS = 2516.6      # MI355X dense fp16 MFMA
 MALL_BYTES = 256 << 20
+# Calibration copy for the PMC byte counters: an fp16 -> fp32 conversion copy of
+# this many elements reads exactly 2x and writes exactly 4x that many bytes.
+COPY_CAL_ELEMS = 64 << 20
+COPY_CAL_KERNEL = "float16tofloat32_copy_kernel"
+DECODE_KERNEL = "linear_decode_kernel"
+PREFILL_KERNEL = "linear_prefill_kernel"
+TRAFFIC_FILE = "decode_gemv_4096x4096_b10_m1_traffic.md"
 
 
 def log(msg: str) -> None:
@@ -46,6 +59,10 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--no-prefill", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--traffic-probe", action="store_true",
+                   help="run eager GEMV/prefill launches and a calibration copy for rocprofv3 --pmc")
+    p.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
+    p.add_argument("--summarize-trace", metavar="KERNEL_STATS_CSV")
     return p.parse_args()
 
 
@@ -194,9 +211,142 @@ def cpu_baseline(layer, seconds: float) -> dict:
                       f"ebo_gemv_f32_baseline, OpenMP over rows; {cores} cores visible"}
 
 
+def traffic_probe(args) -> int:
+    """Eager launches to be counted by `rocprofv3 --pmc FETCH_SIZE` / `WRITE_SIZE`: the
+    headline GEMV over its rotated copies, the prefill GEMM, and COPY_CAL_ELEMS-element
+    fp16 -> fp32 copies whose true read and write bytes are known."""
+    import torch
+
+    rows = cols = 4096
+    layer = compressed_layer(rows, cols, 0.01, 512)
+    mats = copies_of(layer, max(2, -(-2 * MALL_BYTES // layer.matrix.executionBytes) + 1))
+    x = torch.randn(1, cols, generator=torch.Generator().manual_seed(1)).half().cuda()
+    y = torch.empty(1, rows, dtype=torch.float16, device="cuda")
+    for i in range(args.steps):
+        mats[i % len(mats)].forwardTorch(x, out=y)
+    torch.cuda.synchronize()
+    log(f"probe: {args.steps} GEMV launches, b={layer.matrix.storageBits}")
+    src = torch.randn(COPY_CAL_ELEMS, device="cuda").half()
+    dst = torch.empty(COPY_CAL_ELEMS, dtype=torch.float32, device="cuda")
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"probe: 4 calibration copies of {COPY_CAL_ELEMS} fp16 -> fp32 elements")
+    if not args.no_prefill:
+        big = compressed_layer(14336, 4096, 0.01, 512)
+        xp = torch.randn(2048, 4096, generator=torch.Generator().manual_seed(1)).half().cuda()
+        yp = torch.empty(2048, 14336, dtype=torch.float16, device="cuda")
+        for _ in range(4):
+            big.matrix._native.forwardTorch(xp, out=yp)
+        torch.cuda.synchronize()
+        log(f"probe: 4 prefill launches, b={big.matrix.storageBits}")
+    return 0
+
+
+def _pmc_rows(path: str, counter: str) -> dict:
+    """{kernel name: [per-dispatch counter values]} from a rocprofv3 counter_collection.csv."""
+    import collections
+    import csv
+
+    out = collections.defaultdict(list)
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            if r["Counter_Name"] == counter:
+                out[r["Kernel_Name"]].append(float(r["Counter_Value"]))
+    return out
+
+
+def _pick(rows: dict, needle: str) -> list:
+    vals = [v for name, vs in rows.items() if needle in name for v in vs]
+    if not vals:
+        raise SystemExit(f"no dispatch of a kernel named *{needle}* in the counter file")
+    return vals
+
+
+def summarize_pmc(fetch_csv: str, write_csv: str) -> int:
+    """Markdown summary of the FETCH_SIZE and WRITE_SIZE passes (KiB per dispatch),
+    each counter scaled by the factor that maps the calibration copy's reading onto
+    its known bytes.  Prints the GEMV's `traffic_bytes_per_launch` for bench.py."""
+    import statistics
+
+    fetch = _pmc_rows(fetch_csv, "FETCH_SIZE")
+    write = _pmc_rows(write_csv, "WRITE_SIZE")
+    # The calibration copies are the largest fp16->fp32 copies in the run.
+    cf = _pick(fetch, COPY_CAL_KERNEL)
+    cw = _pick(write, COPY_CAL_KERNEL)
+    cf = [v for v in cf if v >= 0.5 * max(cf)]
+    cw = [v for v in cw if v >= 0.5 * max(cw)]
+    true_read, true_write = 2 * COPY_CAL_ELEMS, 4 * COPY_CAL_ELEMS
+    f_fetch = true_read / (statistics.mean(cf) * 1024)
+    f_write = true_write / (statistics.mean(cw) * 1024)
+    lines = [
+        "# HBM traffic per launch: decode GEMV and prefill GEMM (rocprofv3 PMC)",
+        "",
+        "Workloads: decode GEMV 4096x4096, M=1 (BASELINE configs[1], the bench headline); "
+        "prefill GEMM 4096->14336, M=2048 (configs[3]). Weights compressed by ElasticBit.compress "
+        "at threshold 0.01, b selected by the width search.",
+        "",
+        "Commands (one MI355X, repository root):",
+        "",
+        "    timeout -s KILL 120 rocprofv3 --pmc FETCH_SIZE -f csv -d gpurun_out/pmc_fetch -o fetch -- python -u bench.py --traffic-probe --steps 200",
+        "    timeout -s KILL 120 rocprofv3 --pmc WRITE_SIZE -f csv -d gpurun_out/pmc_write -o write -- python -u bench.py --traffic-probe --steps 200",
+        "    python bench.py --summarize-pmc gpurun_out/pmc_fetch/fetch_counter_collection.csv gpurun_out/pmc_write/write_counter_collection.csv",
+        "",
+        f"Calibration: `{COPY_CAL_KERNEL}` over {COPY_CAL_ELEMS} elements reads {true_read} B and "
+        f"writes {true_write} B. It reads FETCH_SIZE {statistics.mean(cf):.1f} KiB and WRITE_SIZE "
+        f"{statistics.mean(cw):.1f} KiB per dispatch ({len(cf)} dispatches), so bytes = "
+        f"FETCH_SIZE x 1024 x {f_fetch:.4f} and WRITE_SIZE x 1024 x {f_write:.4f}.",
+        "",
+        "| kernel | dispatches | FETCH_SIZE KiB (avg) | WRITE_SIZE KiB (avg) | scaled read B | scaled write B | traffic B |",
+        "|---|---|---|---|---|---|---|",
+    ]
+    # One launch of the path may be several dispatches (the prefill runs its
+    # full tiles and its half tiles as two kernels): per-launch traffic sums
+    # the per-dispatch averages of each distinct kernel.
+    result = {}
+    for needle in (DECODE_KERNEL, PREFILL_KERNEL):
+        names = sorted(n for n in fetch if needle in n)
+        if not names:
+            continue
+        total = 0.0
+        for name in names:
+            fv, wv = fetch[name], write.get(name, [0.0])
+            rd = statistics.mean(fv) * 1024 * f_fetch
+            wr = statistics.mean(wv) * 1024 * f_write
+            total += rd + wr
+            short = name.replace("void ", "").replace("(anonymous namespace)::", "").split("(")[0]
+            lines.append(f"| `{short}` | {len(fv)} | {statistics.mean(fv):.1f} | {statistics.mean(wv):.1f} | "
+                         f"{rd:.0f} | {wr:.0f} | {rd + wr:.0f} |")
+        result[needle] = int(round(total))
+    lines.append("")
+    if DECODE_KERNEL in result:
+        lines.append(f"traffic_bytes_per_launch: {result[DECODE_KERNEL]}")
+    if PREFILL_KERNEL in result:
+        lines.append(f"prefill_traffic_bytes_per_launch: {result[PREFILL_KERNEL]}")
+    print("\n".join(lines))
+    return 0
+
+
+def summarize_trace(stats_csv: str) -> int:
+    """Markdown table of the ElasticBit kernels in a rocprofv3 kernel_stats.csv."""
+    import csv
+
+    print("| kernel | calls | avg us | min us | max us |")
+    print("|---|---|---|---|---|")
+    with open(stats_csv, newline="") as f:
+        for r in csv.DictReader(f):
+            name = r["Name"]
+            if "ebk::" not in name:
+                continue
+            short = name.replace("void ", "").replace("(anonymous namespace)::", "").split("(")[0]
+            print(f"| `{short}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.3f} | "
+                  f"{float(r['MinNs']) / 1e3:.3f} | {float(r['MaxNs']) / 1e3:.3f} |")
+    return 0
+
+
 def measured_traffic() -> int | None:
     """HBM bytes per GEMV launch from the committed rocprofv3 PMC summary, if present."""
-    path = ROOT / "profiles" / "gemv_4096x4096_b10_m1_traffic.md"
+    path = ROOT / "profiles" / TRAFFIC_FILE
     if not path.exists():
         return None
     m = re.search(r"traffic_bytes_per_launch:\s*([0-9]+)", path.read_text())
@@ -205,6 +355,10 @@ def measured_traffic() -> int | None:
 
 def main() -> int:
     args = parse_args()
+    if args.summarize_pmc:
+        return summarize_pmc(*args.summarize_pmc)
+    if args.summarize_trace:
+        return summarize_trace(args.summarize_trace)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the ElasticBit path is "
               "benchmarked on a single MI355X.", file=sys.stderr)
@@ -215,6 +369,9 @@ def main() -> int:
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
     import mlbricks_amd.elasticbit._native  # noqa: F401  fail loudly if the HIP library is missing
+
+    if args.traffic_probe:
+        return traffic_probe(args)
 
     g = bench_gemv(args)
     prefill = None if args.no_prefill else bench_prefill(args)

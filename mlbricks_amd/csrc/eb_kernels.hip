@@ -650,10 +650,12 @@ __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// prefill kernel, M > 16: 128 x 128 output tiles, K steps of 64 (two groups).
-// Four waves in a 2 x 2 grid each own 64 x 64.  Every K step the workgroup
-// stages the activation tile and the decoded fp16 weight tile in LDS (double
-// buffered) and feeds v_mfma_f32_16x16x32_f16.
+// general GEMM, M > 16, for what linear_prefill_kernel does not take: raw
+// fp16 weights (b = 16) and activations that are not 16-byte aligned or
+// whose K is not a multiple of 8.  128 x 128 output tiles, K steps of 64
+// (two groups).  Four waves in a 2 x 2 grid each own 64 x 64.  Every K step
+// the workgroup stages the activation tile and the decoded fp16 weight tile
+// in LDS (double buffered) and feeds v_mfma_f32_16x16x32_f16.
 // ---------------------------------------------------------------------------
 
 constexpr int kBM = 128;
@@ -800,19 +802,24 @@ __global__ __launch_bounds__(256) void linear_gemm_kernel(
 // ---------------------------------------------------------------------------
 // prefill kernel (tiled planes), M > 16, integer-dot and decoded-fp16 modes.
 //
-// Workgroup tile: 128 activation rows x 256 weight rows (16 row tiles), K
-// steps of 128 columns (one plane tile).  Each of the four waves owns 64
-// weight rows (four row tiles) for all 128 activation rows: a 128 x 64
-// accumulator tile, 4 x 2 blocks of v_mfma_f32_32x32x16_f16 (the 32x32
-// shape sustains near-peak rate with few independent accumulators; the
-// 16x16x32 shape needs many more).
+// Workgroup tile: 128 activation rows x 128*NB weight rows, K steps of 128
+// columns (one plane tile).  Four column groups of waves each own 32*NB
+// weight rows for all 128 activation rows: a 128 x 32*NB accumulator tile,
+// 4 x NB blocks of v_mfma_f32_32x32x16_f16 (the 32x32 shape sustains
+// near-peak rate with few independent accumulators; the 16x16x32 shape
+// needs many more).  With KS = 2 each column group is two waves (eight
+// waves, two per SIMD) that take the two group pairs of every step and
+// add their partial sums through LDS at the end.  The launcher runs NB = 2
+// (128 x 256) tiles and covers a partial last round of the machine with
+// NB = 1 half tiles.
 //
 //  * B (weights) never goes through LDS.  For weight block nb2 (32 rows =
 //    two row tiles) and group pair p, lane l = 32h + n loads slot
 //    16*(2p+h) + n%16 of row tile 2*nb2 + n/16 -- the B operand rows of
 //    v_mfma_f32_32x32x16_f16 -- and decodes it in registers.  Each decoded
 //    operand feeds four MFMAs (one per 32 activation rows).  B of step k+1
-//    is loaded into a second register buffer while step k is multiplied.
+//    (k+2 for codes of at most 10 bits) is loaded into a register buffer
+//    while step k is multiplied.
 //  * A (activations) goes global -> LDS directly (global_load_lds_dwordx4,
 //    no registers), into a ring of three stages so that step k+2 is in
 //    flight while step k is multiplied.  A stage row is 256 bytes with its
