@@ -650,6 +650,89 @@ __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// GEMV, M = 1, K at most 32 tiles (4096 columns): one workgroup of 16 waves
+// owns one row tile and wave w takes its tiles w and w + 16, so every
+// weight tile of the workgroup is requested at once, before the wave waits
+// for anything.  On MI355X a 4096 x 4096 b = 10 matrix spreads as 16 waves
+// per CU with 5 KB each in flight; the linear_decode_kernel organisation
+// (8 waves, one tile in flight plus one prefetched) takes 7% longer there.
+// For longer rows the all-in-flight form measured slower (more bytes in
+// flight per CU than the memory system serves well), so those keep
+// linear_decode_kernel.
+//
+// Only activation row 0 of the A operand is non-zero, so D[0][n] (lane n,
+// element 0) holds row n's partial sum; the 16 partials of a row are added
+// in wave order, so results are deterministic.
+// ---------------------------------------------------------------------------
+
+constexpr int kGemvWaves = 16;
+constexpr int kGemvMaxSteps = 2 * kGemvWaves;
+
+template <int B, int MODE>
+__global__ __launch_bounds__(64 * kGemvWaves) void linear_gemv_kernel(
+    DevMatrix m, const uint16_t* __restrict__ x, uint16_t* __restrict__ y, const uint16_t* __restrict__ bias) {
+    using Bits = GroupBits<B, MODE>;
+    extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   // [cols], cols % 128 == 0
+    __shared__ float red[kGemvWaves][kTileRows];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int nl = lane & 15;
+    const int quarter = lane >> 4;
+    const int steps = m.spr;
+    const int row = blockIdx.x * kTileRows + nl;
+    float s = 0.0f;
+    if constexpr (MODE == kModeW) s = row < m.rows ? m.scales[row] : 0.0f;
+    float out_scale = 1.0f;
+    uint16_t out_bias = 0;
+    if (threadIdx.x < kTileRows && row < m.rows) {
+        if constexpr (MODE == kModeQ) out_scale = m.scales[row];
+        if (bias) out_bias = bias[row];
+    }
+    // x goes global -> LDS, one 16-byte vector per thread (cols / 8 <= 512)
+    const int nv = m.cols / 8;
+    if (static_cast<int>(threadIdx.x) < nv) {
+        __builtin_amdgcn_global_load_lds(x + 8 * threadIdx.x, (lds_void_ptr)(xs + 8 * (threadIdx.x & ~63u)), 16, 0,
+                                         0);
+    }
+    const size_t slot0 = static_cast<size_t>(blockIdx.x) * steps * kTileSlots + lane;
+    Bits b0, b1;
+    b0.load(m, slot0 + static_cast<size_t>(min(wave, steps - 1)) * kTileSlots);
+    b1.load(m, slot0 + static_cast<size_t>(min(wave + kGemvWaves, steps - 1)) * kTileSlots);
+    // everything but the two weight tiles (scales, bias, x) has landed
+    wait_vmcnt<2 * GroupLoads<B, MODE>::value>();
+    barrier_after_wait();
+
+    floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto mul = [&](const Bits& bits, int st) {
+        const bool ok = st < steps;
+        const int k0 = (min(st, steps - 1) * kTileGroups + quarter) * kGroup;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const half8 xa = *reinterpret_cast<const half8*>(xs + k0 + 8 * t);   // broadcast per quarter
+            const half8 a = (ok && nl == 0) ? xa : half8{0, 0, 0, 0, 0, 0, 0, 0};
+            half8 b = bits.operand(t, s);
+            if constexpr (MODE == kModeRaw) {
+                // past the last tile the reloaded raw weights may hold Inf or NaN
+                if (!ok) b = half8{0, 0, 0, 0, 0, 0, 0, 0};
+            }
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc, 0, 0, 0);
+        }
+    };
+    mul(b0, wave);
+    mul(b1, wave + kGemvWaves);
+
+    if (lane < kTileRows) red[wave][lane] = acc[0];
+    __syncthreads();
+    if (threadIdx.x < kTileRows && row < m.rows) {
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kGemvWaves; ++w) v += red[w][threadIdx.x];
+        y[row] = epilogue<MODE>(v, out_scale, bias != nullptr, out_bias);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // general GEMM, M > 16, for what linear_prefill_kernel does not take: raw
 // fp16 weights (b = 16) and activations that are not 16-byte aligned or
 // whose K is not a multiple of 8.  128 x 128 output tiles, K steps of 64
@@ -1327,11 +1410,21 @@ constexpr int kPrefillKS = EBK_PREFILL_KS;
 constexpr int kDecodeWaves = EBK_DECODE_WAVES;
 constexpr int kDecodeGpl = EBK_DECODE_GPL;
 constexpr int kDecodeMaxM = 16;
+// Modes the GEMV kernel takes (bit per Mode).  The decoded-fp16 mode
+// (b >= 11, fullPrecision) spends ~7 VALU instructions per code on the fp32
+// product and its rounding; at four waves per SIMD that work is exposed, and
+// linear_decode_kernel is faster for it (8.7 vs 9.6 us at 4096 x 4096 b = 15).
+#ifndef EBK_GEMV_MODES
+#define EBK_GEMV_MODES ((1 << kModeQ) | (1 << kModeRaw))
+#endif
 
 template <int B, int MODE>
 hipError_t run_linear_mode(const DevMatrix& m, const uint16_t* x, int64_t M, uint16_t* y,
                            const uint16_t* bias, int xvec, hipStream_t s) {
-    if (M <= kDecodeMaxM) {
+    if (M == 1 && xvec == 2 && m.spr <= kGemvMaxSteps && ((EBK_GEMV_MODES >> MODE) & 1)) {
+        hipLaunchKernelGGL((linear_gemv_kernel<B, MODE>), dim3(m.rtiles), dim3(64 * kGemvWaves),
+                           static_cast<size_t>(m.cols) * 2, s, m, x, y, bias);
+    } else if (M <= kDecodeMaxM) {
         const size_t xbytes = static_cast<size_t>(M) * m.spr * kTileGroups * kGroup * 2;
         if (xbytes <= static_cast<size_t>(kXLdsBytes)) {
             hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, true>), dim3(m.rtiles),

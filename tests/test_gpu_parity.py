@@ -132,6 +132,55 @@ def test_one_hot_activations_reproduce_decoded_weights(native, b, M, policy):
     assert np.array_equal(y, dec16[:, ks].T)
 
 
+@pytest.mark.parametrize("b", list(range(3, 16)) + [16])
+@pytest.mark.parametrize("rows,cols", [(1, 128), (17, 384), (100, 2048), (33, 4096), (16, 4224)])
+@pytest.mark.parametrize("policy", ["hardwareNative", "fullPrecision"])
+def test_gemv_whole_tile_rows(native, b, rows, cols, policy):
+    """M = 1 with 16-byte aligned x and whole 128-column tiles: the 16-wave
+    GEMV kernel up to 4096 columns (4224 takes the pipelined decode kernel),
+    against the oracle, with and without bias."""
+    rng = np.random.default_rng(b * 7 + rows + cols)
+    if b == 16:
+        w = (rng.standard_normal((rows, cols)) * 0.05).astype(np.float32)
+        m = native.RuntimeMatrix._compressSelected(w, 16, 0.01, 0.0, decodePolicy=policy)
+        payload, s = ora.pack_weights(w, 16), None
+    else:
+        q = _codes(rng, rows, cols, b)
+        s = rng.uniform(0.002, 0.05, size=rows).astype(np.float32)
+        m = native.RuntimeMatrix._compressSelectedCodes(q, s, b, 0.01, 0.0, decodePolicy=policy)
+        payload = ora.pack_codes(q, b)
+    x = _x16(rng, 1, cols)
+    assert x.data_ptr() % 16 == 0
+    y = m.forwardTorch(x)
+    ref = _reference(payload, s, rows, cols, b, x.cpu().numpy().view(np.uint16), policy)
+    assert _rel_max(y.float().cpu().numpy(), ref) <= TOL
+    bias = torch.from_numpy(rng.standard_normal(rows).astype(np.float16)).cuda()
+    assert torch.equal(m.forwardTorch(x, bias=bias), y + bias)
+
+
+@pytest.mark.parametrize("b", [3, 4, 9, 10, 11, 15, 16])
+@pytest.mark.parametrize("policy", ["hardwareNative", "fullPrecision"])
+def test_gemv_one_hot_reproduces_decoded_weights(native, b, policy):
+    """M = 1 one-hot activations through the GEMV kernel: y[n] is the decoded
+    weight w[n][k] (or fp16(s*q) in integer-dot mode, the same bits)."""
+    rows, cols = 40, 512
+    rng = np.random.default_rng(b)
+    if b == 16:
+        w = (rng.standard_normal((rows, cols)) * 0.05).astype(np.float32)
+        m = native.RuntimeMatrix._compressSelected(w, 16, 0.01, 0.0, decodePolicy=policy)
+        dec16 = w.astype(np.float16).view(np.uint16)
+    else:
+        q = _codes(rng, rows, cols, b)
+        s = rng.choice([1e-7, 3e-5, 0.01, 0.37], size=rows).astype(np.float32)
+        m = native.RuntimeMatrix._compressSelectedCodes(q, s, b, 0.01, 0.0, decodePolicy=policy)
+        _, dec16 = ora.dequantize(ora.pack_codes(q, b), s, rows, cols, b)
+    for k in (0, 127, 128, 300, cols - 1):
+        x = torch.zeros(1, cols, dtype=torch.float16, device="cuda")
+        x[0, k] = 1.0
+        y = m.forwardTorch(x).cpu().numpy().view(np.uint16)
+        assert np.array_equal(y[0], dec16[:, k]), f"k={k}"
+
+
 @pytest.mark.parametrize("b", [4, 10, 13])
 @pytest.mark.parametrize("rows,cols", [(1, 1), (7, 13), (8, 31), (17, 32), (33, 65), (5, 1000)])
 @pytest.mark.parametrize("M", [1, 5, 40])
