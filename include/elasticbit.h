@@ -184,6 +184,17 @@ int eb_packed_linear(const void* x, int x_dtype, int64_t M, const uint8_t* packe
                      int64_t group_size, int64_t out_features, int64_t in_features,
                      void* y, void* stream);
 
+/* Tuning control (no counterpart in the reference, which hands M > 1 to the
+ * vendor GEMM): the output tile shape of the prefill route (M > 16, b <= 10,
+ * hardwareNative or fullPrecision).  EB_PREFILL_TILES_AUTO (the default)
+ * picks the shape with the fewer estimated rounds over the GPU's compute
+ * units; NARROW forces 128 x 256 tiles; WIDE forces 256 x 256 tiles where M
+ * and rows are both at least 256.  Results agree within the output
+ * tolerance either way; the sum order differs.  Process-wide, read at each
+ * launch. */
+enum { EB_PREFILL_TILES_AUTO = 0, EB_PREFILL_TILES_NARROW = 1, EB_PREFILL_TILES_WIDE = 2 };
+int eb_set_prefill_tiles(int mode);
+
 /* ---- host codec (the packer inside the RuntimeMatrix constructors) --------- */
 
 /* pack_exact_codes, runtime.cu:150-186.  payload_bytes must equal

@@ -963,6 +963,14 @@ int eb_packed_linear(const void* x, int x_dtype, int64_t M, const uint8_t* packe
     });
 }
 
+int eb_set_prefill_tiles(int mode) {
+    return guarded([&] {
+        require(mode == EB_PREFILL_TILES_AUTO || mode == EB_PREFILL_TILES_NARROW || mode == EB_PREFILL_TILES_WIDE,
+                "prefill tile mode must be auto (0), narrow (1) or wide (2)");
+        ebk::set_prefill_tiles(mode);
+    });
+}
+
 int eb_host_pack_codes(const int16_t* codes, uint64_t count, int bits, uint8_t* payload, uint64_t payload_bytes) {
     return guarded([&] {
         require(codes && payload, "pack: null pointer");

@@ -101,6 +101,9 @@ hipError_t launch_materialize(const DevMatrix& m, uint16_t* out, hipStream_t str
 hipError_t launch_linear(const DevMatrix& m, bool exact_w16, const uint16_t* x, int64_t M,
                          uint16_t* y, const uint16_t* bias, hipStream_t stream);
 
+// Prefill tile shape: 0 auto, 1 128 x 256, 2 256 x 256 (process-wide).
+void set_prefill_tiles(int mode);
+
 // Legacy flat-group op (bolt/ops_cuda.cu:2708-2795).
 hipError_t launch_packed_linear(const void* x, int x_dtype, int64_t M, const uint8_t* packed,
                                 const void* scales, int scale_dtype, const void* bias, int bits,

@@ -10,6 +10,13 @@
 // All sums accumulate in fp32 on the matrix cores.
 #include "eb_internal.h"
 
+#include <atomic>
+#include <type_traits>
+
+#ifndef W_ILV
+#define W_ILV 0
+#endif
+
 #include <hip/hip_runtime.h>
 
 namespace ebk {
@@ -424,6 +431,23 @@ template <int B, int MODE>
 struct GroupBits {
     Raw<B> r;
     __device__ __forceinline__ void load(const DevMatrix& m, size_t g) { raw_load<B>(m, g, r); }
+    // Copy of the planes width B has (the others are never written).
+    __device__ __forceinline__ void copy_from(const GroupBits& o) {
+        using P = Planes<B>;
+        if constexpr (P::h8) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) r.d8[i] = o.r.d8[i];
+        }
+        if constexpr (P::h4) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) r.d4[i] = o.r.d4[i];
+        }
+        if constexpr (P::h2) {
+            r.d2[0] = o.r.d2[0];
+            r.d2[1] = o.r.d2[1];
+        }
+        if constexpr (P::h1) r.d1 = o.r.d1;
+    }
     __device__ __forceinline__ void load32(const DevMatrix& m, uint32_t g) { raw_load32<B>(m, g, r); }
     __device__ __forceinline__ half8 operand(int t, float s) const { return decode8<B, MODE>(r, t, s); }
 };
@@ -1254,6 +1278,294 @@ __global__ __launch_bounds__(256 * KS) void linear_prefill_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// prefill, wide tiles (b <= 10): 256 activation rows x 256 weight rows per
+// workgroup, four waves, one per SIMD.  Wave w owns weight rows
+// 64w .. 64w + 63 of the tile for all 256 activation rows: 8 x 2 blocks of
+// v_mfma_f32_32x32x16_f16 (256 accumulator registers per lane).
+//
+// Why this shape: per K step (128 columns) the CU moves 64 KB of activations
+// (global -> LDS, shared by the four waves) and 40 KB of b = 10 weight bits
+// (global -> registers, each wave its own 64 rows, nothing loaded twice)
+// for 512 MFMAs; the 128 x 256 tile of linear_prefill_kernel moves 72 KB
+// for 256, and the CU's vector memory pipe (64 B per clock) was what its
+// waves stalled on.  Each decoded weight operand feeds eight MFMAs, each
+// activation operand read from LDS two.
+//
+// Pipeline, per step st (8 slices of 16 columns; slice ps is group pair
+// ps/4, codes 8*(ps%4)..+8):
+//  * the operands of slice ps + 1 (A from LDS, B decoded in registers) are
+//    prepared while the 16 MFMAs of slice ps run;
+//  * activations go global -> LDS into two 64 KB stages; A(st+1) is issued
+//    during slices 0..3 of step st, four 1 KB loads per slice;
+//  * weight bits sit in a register ring of three half steps (a half step is
+//    one group pair of one step: two groups per lane).  Those of half step
+//    h + 2 are loaded in the first two slices of half step h, so every load
+//    has at least five slices to land;
+//  * the workgroup barrier sits before slice 7: by then every A read of the
+//    step's stage has returned and A(st+1) has landed, and slice 7's MFMAs
+//    overlap the first operand reads of step st + 1.
+// Vector loads retire in issue order, so each wait is a count of the loads
+// issued after the ones it needs.
+// ---------------------------------------------------------------------------
+
+constexpr int kWRows = 256;                 // activation rows per workgroup
+constexpr int kWN = 256;                    // weight rows per workgroup (4 waves x 64)
+constexpr int kWHalfRow = kPRow / 2;        // bytes per staged row of a half step (64 columns)
+constexpr int kWHalf = kWRows * kWHalfRow;  // bytes per half-stage (32 KB)
+constexpr int kWGroupM = 4;                 // activation blocks per tile-order group
+
+template <int B, int MODE>
+__global__ __launch_bounds__(256) void linear_prefill_wide_kernel(
+    DevMatrix m, const uint16_t* __restrict__ x, int M, uint16_t* __restrict__ y,
+    const uint16_t* __restrict__ bias, int mblocks, int nblocks, int njobs, int per_xcd) {
+    static_assert(MODE != kModeRaw && B <= 10, "wide tiles hold at most ten bit-plane dwords per group");
+    using Bits = GroupBits<B, MODE>;
+    constexpr int GL = group_loads<B>();           // vector loads per group
+    __shared__ __attribute__((aligned(16))) uint8_t xs[4 * kWHalf];
+
+    const int xcd = blockIdx.x & 7;
+    const int local = blockIdx.x >> 3;
+    const int job = xcd * per_xcd + local;
+    if (local >= per_xcd || job >= njobs) return;
+    const int group = job / (kWGroupM * nblocks);
+    const int within = job - group * kWGroupM * nblocks;
+    const int gm = min(kWGroupM, mblocks - group * kWGroupM);
+    const int mb = group * kWGroupM + within % gm;
+    const int nb = within / gm;
+    const int m0 = mb * kWRows;
+    const int n0 = nb * kWN;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n32 = lane & 31;
+    const int half = lane >> 5;
+    const int steps = m.spr;
+    const int nw0 = n0 + wave * 64;
+
+    // B slots [j][p]: 32-row block j (row tiles nw0/16 + 2j, +1), group pair p.
+    uint32_t slot0[2][2];
+    float s[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int rt = min(nw0 / kTileRows + 2 * j + (n32 >> 4), m.rtiles - 1);
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            slot0[j][p] = static_cast<uint32_t>(rt) * static_cast<uint32_t>(steps * kTileSlots) +
+                          static_cast<uint32_t>(16 * (2 * p + half) + (n32 & 15));
+        }
+        s[j] = 0.0f;
+        if constexpr (MODE == kModeW) {
+            const int row = rt * kTileRows + (n32 & 15);
+            s[j] = row < m.rows ? m.scales[row] : 0.0f;
+        }
+    }
+
+    // A: half step h (columns 64*(h%2) .. +63 of step h/2) of all 256 rows
+    // goes global -> LDS into half-stage h % 4 (32 KB, rows of 128 B).
+    // Wave w fills rows 64w .. 64w + 63, eight rows (1 KB) per instruction;
+    // lane l writes physical chunk l%8 of row l/8, which holds logical chunk
+    // (l%8) ^ ((row >> 1) & 7): with that swizzle the 16 rows read by lanes
+    // 0..15 of an operand read land on distinct banks.  The launcher
+    // guarantees cols % 8 == 0, a 16-byte aligned x and M * cols * 2 below
+    // 4 GiB.
+    int achunk[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) achunk[i] = 8 * ((lane & 7) ^ ((4 * i + (lane >> 4)) & 7));
+    const int arow0 = m0 + wave * 64 + (lane >> 3);
+    const uint8_t* xb = reinterpret_cast<const uint8_t*>(x);
+    auto load_a = [&](int h, int i) {
+        const int k0 = min(h >> 1, steps - 1) * kPK + (h & 1) * (kPK / 2);
+        const uint32_t row = static_cast<uint32_t>(min(arow0 + 8 * i, M - 1));
+        const uint32_t off = 2u * (row * static_cast<uint32_t>(m.cols) +
+                                   static_cast<uint32_t>(min(k0 + achunk[i & 1], m.cols - 8)));
+        __builtin_amdgcn_global_load_lds(
+            xb + off, (lds_void_ptr)(xs + (h & 3) * kWHalf + (wave * 64 + 8 * i) * kWHalfRow), 16, 0, 0);
+    };
+    // weight bits of half step h, block j, into ring buffer r
+    auto load_b = [&](Bits (&r)[2], int h, int j) {
+        const uint32_t st = static_cast<uint32_t>(min(h >> 1, steps - 1));
+        r[j].load32(m, slot0[j][h & 1] + st * kTileSlots);
+    };
+
+    floatx16 acc[8][2];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    // Operands.  The A operands of a slice are two halves of four row
+    // blocks; each half is single-buffered: the high half of slice q is read
+    // while the low-half MFMAs run, the low half of slice q + 1 while the
+    // high-half MFMAs run.  The B operands (two decoded blocks) are
+    // double-buffered by set.  set, hh and q are constants at every call, so
+    // the arrays stay in registers.
+    half8 pa[2][4], pb[2][2];
+    const int aswz = (n32 >> 1) & 7;
+    auto read_a = [&](int hh, int h, int q) {
+        const int chunk = (4 * half + q) ^ aswz;
+        const uint8_t* base = xs + (h & 3) * kWHalf + (128 * hh + n32) * kWHalfRow + chunk * 16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pa[hh][i] = *reinterpret_cast<const half8*>(base + 32 * i * kWHalfRow);
+    };
+    auto decode_b = [&](int set, int j, int q, const Bits (&r)[2]) { pb[set][j] = r[j].operand(q, s[j]); };
+    auto mfma_half = [&](int hh, int set) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                acc[4 * hh + i][j] =
+                    __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[hh][i], pb[set][j], acc[4 * hh + i][j], 0, 0, 0);
+    };
+
+    // Half step h: four slices of 16 columns (codes 8q .. 8q + 7 of the
+    // lane's group).  rc: its weight bits; rn: the bits of half step h + 1;
+    // rf: the free ring buffer, filled with half step h + 2.  Every slice
+    // issues two of the eight A loads of half step h + 2, slices 0 and 1 one
+    // weight group each, so each CU's vector memory pipe sees an even load.
+    //
+    // Slice q, entered with A-low(q) read and B(q) decoded into set q % 2:
+    //   loads; read A-high(q); wait A-low(q); low MFMAs + decode B(q+1)
+    //   block 0; wait A-high(q); read A-low(q+1); high MFMAs + decode
+    //   B(q+1) block 1.
+    // Slice 3 instead waits for every load older than this half step's, so
+    // that A and B of half step h + 1 have landed, and passes the workgroup
+    // barrier before reading half-stage (h+1) % 4; its high-half MFMAs
+    // overlap both decodes of slice 0 of half step h + 1.  The barrier also
+    // retires every read of half-stage h % 4 before half step h + 1 refills
+    // it... with the loads of half step h + 4, two half steps later.
+    auto half_step = [&](const Bits (&rc)[2], const Bits (&rn)[2], Bits (&rf)[2], int h) {
+        const bool more = h + 1 < 2 * steps;
+        auto slice = [&](auto q_c) {
+            constexpr int Q = decltype(q_c)::value;
+            constexpr int SET = Q & 1;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) load_a(h + 2, 2 * Q + i);
+            if constexpr (Q < 2) load_b(rf, h + 2, Q);
+            __builtin_amdgcn_sched_barrier(0);
+            read_a(1, h, Q);
+            wait_lgkmcnt<4>();                     // A-low(q) landed
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_half(0, SET);
+            if constexpr (Q < 3) decode_b(SET ^ 1, 0, Q + 1, rc);
+            __builtin_amdgcn_sched_barrier(0);
+            wait_lgkmcnt<0>();                     // A-high(q) landed
+            if constexpr (Q == 3) {
+                // A and B of half step h + 1 landed: the younger loads are
+                // the eight A loads and two B groups of this half step
+                wait_vmcnt<8 + 2 * GL>();
+                barrier_after_wait();
+                __builtin_amdgcn_sched_barrier(0);
+                if (more) read_a(0, h + 1, 0);
+            } else {
+                read_a(0, h, Q + 1);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_half(1, SET);
+            if constexpr (Q < 3) {
+                decode_b(SET ^ 1, 1, Q + 1, rc);
+            } else {
+                if (more) {
+                    decode_b(0, 0, 0, rn);
+                    decode_b(0, 1, 0, rn);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        slice(std::integral_constant<int, 0>{});
+        slice(std::integral_constant<int, 1>{});
+        slice(std::integral_constant<int, 2>{});
+        slice(std::integral_constant<int, 3>{});
+    };
+
+    Bits ring0[2], ring1[2], ring2[2];
+    // prologue: half steps 0 and 1 (A and B)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) load_a(0, i);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) load_b(ring0, 0, j);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) load_a(1, i);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) load_b(ring1, 1, j);
+    wait_vmcnt<0>();
+    barrier_after_wait();
+    read_a(0, 0, 0);
+    decode_b(0, 0, 0, ring0);
+    decode_b(0, 1, 0, ring0);
+    // One step (two half steps) per iteration.  The ring advances by two
+    // buffers per step, (r0, r1, r2) <- (r2, r0, r1), by register copies
+    // (at most 20 moves per step).  A loop body of three steps with an
+    // exit after each needs no copies, but the accumulator merges at those
+    // exits overflow the 256 accumulator registers and spill.
+    for (int st = 0; st < steps; ++st) {
+        half_step(ring0, ring1, ring2, 2 * st);
+        half_step(ring1, ring2, ring0, 2 * st + 1);
+        Bits t[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            t[j].copy_from(ring0[j]);
+            ring0[j].copy_from(ring2[j]);
+            ring2[j].copy_from(ring1[j]);
+            ring1[j].copy_from(t[j]);
+        }
+    }
+
+    // ---- epilogue: two passes of 128 activation rows through LDS ----
+    // 32x32 block element e of lane l is D[8*(e/4) + 4*(l/32) + e%4][l%32].
+    // The clamped re-loads of the last step must land before the LDS is
+    // reused.
+    wait_vmcnt<0>();
+    __syncthreads();
+    constexpr int kCPitch = 2 * kWN + 16;       // bytes per staged output row
+    static_assert(128 * kCPitch <= 4 * kWHalf, "output staging exceeds the activation LDS");
+    float sn[2];
+    uint16_t bn[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int n = min(nw0 + 32 * j + n32, m.rows - 1);
+        sn[j] = 1.0f;
+        bn[j] = 0;
+        if constexpr (MODE == kModeQ) sn[j] = m.scales[n];
+        if (bias) bn[j] = bias[n];
+    }
+    const bool yvec = (m.rows % 8 == 0) && (reinterpret_cast<uintptr_t>(y) % 16 == 0);
+    const int chunk = threadIdx.x & 31;         // 16-byte chunk of a 512-byte row
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+        if (pass > 0) __syncthreads();
+        uint8_t* cw = xs + wave * 128;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int r = 32 * i + 8 * (e >> 2) + 4 * half + (e & 3);
+                    *reinterpret_cast<uint16_t*>(cw + r * kCPitch + (32 * j + n32) * 2) =
+                        epilogue<MODE>(acc[4 * pass + i][j][e], sn[j], bias != nullptr, bn[j]);
+                }
+        __syncthreads();
+#pragma unroll 2
+        for (int it = 0; it < 16; ++it) {
+            const int r = it * 8 + (threadIdx.x >> 5);
+            const int gr = m0 + pass * 128 + r;
+            const int gn = n0 + chunk * 8;
+            if (gr >= M || gn >= m.rows) continue;
+            const uint4 v = *reinterpret_cast<const uint4*>(xs + r * kCPitch + chunk * 16);
+            uint16_t* dst = y + static_cast<size_t>(gr) * m.rows + gn;
+            if (yvec) {
+                *reinterpret_cast<uint4*>(dst) = v;
+            } else {
+                const uint16_t* hh = reinterpret_cast<const uint16_t*>(&v);
+                for (int k = 0; k < 8 && gn + k < m.rows; ++k) dst[k] = hh[k];
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // legacy flat-group op (bolt/ops_cuda.cu:2708-2750): one wave per output
 // feature, four activation rows per wave, lanes stride over K.
 // ---------------------------------------------------------------------------
@@ -1414,9 +1726,31 @@ constexpr int kDecodeMaxM = 16;
 // (b >= 11, fullPrecision) spends ~7 VALU instructions per code on the fp32
 // product and its rounding; at four waves per SIMD that work is exposed, and
 // linear_decode_kernel is faster for it (8.7 vs 9.6 us at 4096 x 4096 b = 15).
+#ifndef EBK_PREFILL_WIDE
+#define EBK_PREFILL_WIDE 1
+#endif
 #ifndef EBK_GEMV_MODES
 #define EBK_GEMV_MODES ((1 << kModeQ) | (1 << kModeRaw))
 #endif
+
+// Whether the 256 x 256 prefill tiles finish before the 128 x 256 ones.
+// Cost in rounds of 128 x 256 tiles over the CUs: a 256 x 256 tile takes
+// about 1.7 of them (measured on MI355X, 14336 x 4096 b = 10: 116 us per
+// wide round, 68 us per narrow round); the narrow kernel runs a last round
+// that would leave half the CUs idle as half tiles, at about two thirds of
+// a round.
+std::atomic<int> g_prefill_tiles{0};   // eb_set_prefill_tiles
+
+inline bool prefer_wide_tiles(int64_t M, int rows, int cus) {
+    const int mode = g_prefill_tiles.load(std::memory_order_relaxed);
+    if (mode != 0) return mode == 2;
+    const int64_t wide = ((M + kWRows - 1) / kWRows) * ((rows + kWN - 1) / kWN);
+    const int64_t narrow = ((M + 127) / 128) * ((rows + kPN - 1) / kPN);
+    const double t_wide = 1.7 * static_cast<double>((wide + cus - 1) / cus);
+    const int64_t rem = narrow % cus;
+    const double t_narrow = static_cast<double>(narrow / cus) + (rem == 0 ? 0.0 : (2 * rem <= cus ? 0.67 : 1.0));
+    return t_wide < t_narrow;
+}
 
 template <int B, int MODE>
 hipError_t run_linear_mode(const DevMatrix& m, const uint16_t* x, int64_t M, uint16_t* y,
@@ -1432,6 +1766,17 @@ hipError_t run_linear_mode(const DevMatrix& m, const uint16_t* x, int64_t M, uin
         } else {
             hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, false>), dim3(m.rtiles),
                                dim3(64 * kDecodeWaves), 0, s, m, x, static_cast<int>(M), y, bias, xvec);
+        }
+    } else if (MODE != kModeRaw && B <= 10 && EBK_PREFILL_WIDE && xvec && M >= kWRows && m.rows >= kWN &&
+               static_cast<uint64_t>(M) * m.cols * 2 < (uint64_t(1) << 32) &&
+               prefer_wide_tiles(M, m.rows, device_cu_count())) {
+        if constexpr (MODE != kModeRaw && B <= 10) {
+            const int mblocks = static_cast<int>((M + kWRows - 1) / kWRows);
+            const int nblocks = (m.rows + kWN - 1) / kWN;
+            const int jobs = mblocks * nblocks;
+            const int per_xcd = (jobs + 7) / 8;
+            hipLaunchKernelGGL((linear_prefill_wide_kernel<B, MODE>), dim3(8 * per_xcd), dim3(256), 0, s, m, x,
+                               static_cast<int>(M), y, bias, mblocks, nblocks, jobs, per_xcd);
         }
     } else if (MODE != kModeRaw && xvec && static_cast<uint64_t>(M) * m.cols * 2 < (uint64_t(1) << 32)) {
         if constexpr (MODE != kModeRaw) {
@@ -1498,6 +1843,8 @@ hipError_t launch_repack(const uint8_t* canon, uint64_t canon_bytes, const DevMa
     }
     return dispatch_bits<RepackOp>(out.bits, canon, canon_bytes, out, stream);
 }
+
+void set_prefill_tiles(int mode) { g_prefill_tiles.store(mode, std::memory_order_relaxed); }
 
 hipError_t launch_unpack(const DevMatrix& m, int16_t* out, hipStream_t stream) {
     return dispatch_bits<UnpackOp>(m.bits, m, out, stream);

@@ -98,6 +98,7 @@ _sig("eb_forward", [_vp, _vp, _i64, _vp, _vp, _vp])
 _sig("eb_materialize_fp16", [_vp, _vp, _vp])
 _sig("eb_unpack_codes", [_vp, _vp, _vp])
 _sig("eb_packed_linear", [_vp, _i, _i64, _vp, _vp, _i, _vp, _i, _i64, _i64, _i64, _vp, _vp])
+_sig("eb_set_prefill_tiles", [_i])
 _sig("eb_host_pack_codes", [_i16p, _u64, _i, _u8p, _u64])
 _sig("eb_host_unpack_codes", [_u8p, _u64, _u64, _i, _i16p])
 
@@ -195,6 +196,19 @@ def backendInfo() -> dict:
         "decodeValidation": b.decode_validation.decode(),
         "validated": bool(b.validated),
     }
+
+
+PREFILL_TILES = {"auto": 0, "narrow": 1, "wide": 2}
+
+
+def set_prefill_tiles(mode: str) -> None:
+    """Tile shape of the prefill route (M > 16, b <= 10): 'auto' (default,
+    picked by estimated rounds over the compute units), 'narrow' (128 x 256)
+    or 'wide' (256 x 256).  Process-wide; a tuning and test control with no
+    counterpart in the reference."""
+    if mode not in PREFILL_TILES:
+        raise ValueError(f"prefill tile mode must be one of {sorted(PREFILL_TILES)}")
+    check(_lib.eb_set_prefill_tiles(PREFILL_TILES[mode]))
 
 
 def host_pack_codes(codes: np.ndarray, bits: int) -> np.ndarray:

@@ -208,3 +208,12 @@ def test_device_calls_fail_loudly_without_device():
         m.forward(np.zeros(32, np.float32))
     with pytest.raises(RuntimeError, match="CUDA runtime"):
         m._materializeTorch()
+
+
+def test_prefill_tile_mode_is_validated():
+    with pytest.raises(ValueError, match="prefill tile mode"):
+        native.set_prefill_tiles("square")
+    lib = native.lib()
+    assert lib.eb_set_prefill_tiles(3) != 0
+    for mode in ("narrow", "wide", "auto"):
+        native.set_prefill_tiles(mode)

@@ -353,13 +353,76 @@ def test_legacy_packed_linear_dtypes_and_torch_op(native, dtype):
 # shapes hit: only half tiles (108 tiles), only whole tiles (204), and a mix
 # (308 = 256 whole + 52 split), each with a partial K step, in both the
 # integer-dot and the decoded-fp16 arithmetic.
+@pytest.fixture
+def wide_tiles(native):
+    """Force the 256 x 256 prefill tiles for one test (the automatic choice
+    takes them only for large grids)."""
+    native.set_prefill_tiles("wide")
+    yield
+    native.set_prefill_tiles("auto")
+
+
+@pytest.mark.parametrize("b", [3, 4, 5, 7, 8, 9, 10])
+@pytest.mark.parametrize("rows,cols,M", [(256, 128, 256), (300, 384, 700), (1000, 1000, 513), (520, 4096, 300)])
+@pytest.mark.parametrize("policy", ["hardwareNative", "fullPrecision"])
+def test_wide_prefill_tiles_match_oracle(native, wide_tiles, b, rows, cols, M, policy):
+    """M and rows of at least 256 with b <= 10: the 256 x 256 prefill tiles,
+    ragged in M, N and K (1000 columns are not whole 128-column steps),
+    against the fp64 oracle on a corner and torch fp32 on the whole output,
+    with and without bias."""
+    rng = np.random.default_rng(b * 1000 + rows + cols + M)
+    q = _codes(rng, rows, cols, b)
+    s = rng.uniform(0.002, 0.05, size=rows).astype(np.float32)
+    m = native.RuntimeMatrix._compressSelectedCodes(q, s, b, 0.01, 0.0, decodePolicy=policy)
+    x = _x16(rng, M, cols)
+    y = m.forwardTorch(x)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y).all()
+    wd = m._materializeTorch().float()
+    full = torch.matmul(x.float(), wd.T.contiguous())
+    assert float((y.float() - full).abs().max() / full.abs().max()) <= TOL
+    sub_r, sub_m = 40, 48
+    ref = _reference(ora.pack_codes(q[-sub_r:], b), s[-sub_r:], sub_r, cols, b,
+                     x[-sub_m:].cpu().numpy().view(np.uint16), policy)
+    assert _rel_max(y[-sub_m:, -sub_r:].float().cpu().numpy(), ref) <= TOL
+    bias = torch.from_numpy(rng.standard_normal(rows).astype(np.float16)).cuda()
+    assert torch.equal(m.forwardTorch(x, bias=bias), y + bias)
+
+
+@pytest.mark.parametrize("b", [4, 8, 10])
+@pytest.mark.parametrize("policy", ["hardwareNative", "fullPrecision"])
+def test_wide_prefill_one_hot_reproduces_decoded_weights(native, wide_tiles, b, policy):
+    """One-hot activations through the 256 x 256 prefill tiles: every output
+    is one decoded weight, bit for bit."""
+    rows, cols, M = 300, 640, 512
+    rng = np.random.default_rng(b + 77)
+    q = _codes(rng, rows, cols, b)
+    s = rng.choice([1e-7, 3e-5, 0.01, 0.37], size=rows).astype(np.float32)
+    m = native.RuntimeMatrix._compressSelectedCodes(q, s, b, 0.01, 0.0, decodePolicy=policy)
+    _, dec16 = ora.dequantize(ora.pack_codes(q, b), s, rows, cols, b)
+    ks = rng.integers(0, cols, size=M)
+    x = torch.zeros(M, cols, dtype=torch.float16, device="cuda")
+    x[torch.arange(M), torch.from_numpy(ks).cuda()] = 1.0
+    y = m.forwardTorch(x).cpu().numpy().view(np.uint16)
+    assert np.array_equal(y, dec16[:, ks].T)
+
+
 @pytest.mark.parametrize("rows,cols,M,b,policy", [
     (3000, 1000, 1100, 7, "hardwareNative"),
     (2900, 1000, 2100, 10, "hardwareNative"),
     (7000, 520, 1300, 12, "hardwareNative"),
     (7000, 520, 1300, 9, "fullPrecision"),
 ])
-def test_prefill_tiling_shapes_match_decoded_product(native, rows, cols, M, b, policy):
+@pytest.mark.parametrize("tiles", ["narrow", "auto"])
+def test_prefill_tiling_shapes_match_decoded_product(native, rows, cols, M, b, policy, tiles):
+    native.set_prefill_tiles(tiles)
+    try:
+        _check_prefill_shape(native, rows, cols, M, b, policy)
+    finally:
+        native.set_prefill_tiles("auto")
+
+
+def _check_prefill_shape(native, rows, cols, M, b, policy):
     rng = np.random.default_rng(rows + cols + M + b)
     q = _codes(rng, rows, cols, b)
     s = rng.uniform(0.002, 0.05, size=rows).astype(np.float32)
