@@ -277,6 +277,22 @@ __global__ void repack16_kernel(const uint16_t* __restrict__ canon, DevMatrixOut
 // unpack / materialize (one thread per group)
 // ---------------------------------------------------------------------------
 
+// A group's 32 outputs (2 bytes each) as four 16-byte stores when the group
+// lies inside the row and the row start is 16-byte aligned (cols % 8 == 0);
+// element by element otherwise.
+__device__ __forceinline__ void store_group(uint16_t* __restrict__ dst, int col0, int cols, const uint32_t (&w)[16]) {
+    if (col0 + kGroup <= cols && cols % 8 == 0) {
+        uint4* d = reinterpret_cast<uint4*>(dst + col0);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) d[v] = make_uint4(w[4 * v], w[4 * v + 1], w[4 * v + 2], w[4 * v + 3]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < kGroup; ++i) {
+            if (col0 + i < cols) dst[col0 + i] = static_cast<uint16_t>(w[i >> 1] >> (16 * (i & 1)));
+        }
+    }
+}
+
 template <int B>
 __global__ void unpack_kernel(DevMatrix m, int16_t* __restrict__ out, uint64_t slots) {
     const uint64_t g = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -287,18 +303,21 @@ __global__ void unpack_kernel(DevMatrix m, int16_t* __restrict__ out, uint64_t s
     if (row >= m.rows || col0 >= m.cols) return;
     Raw<B> r;
     raw_load<B>(m, g, r);
-    int16_t* dst = out + static_cast<uint64_t>(row) * m.cols;
+    uint32_t w[16];
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
         uint32_t lo, hi;
         quad_bytes<B>(r, d, lo, hi);
+        uint32_t q[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int col = col0 + 4 * d + j;
             const int u = static_cast<int>(((lo >> (8 * j)) & 0xFFu) | (((hi >> (8 * j)) & 0xFFu) << 8));
-            if (col < m.cols) dst[col] = static_cast<int16_t>(u - Planes<B>::qmax);
+            q[j] = static_cast<uint16_t>(static_cast<int16_t>(u - Planes<B>::qmax));
         }
+        w[2 * d] = q[0] | (q[1] << 16);
+        w[2 * d + 1] = q[2] | (q[3] << 16);
     }
+    store_group(reinterpret_cast<uint16_t*>(out) + static_cast<uint64_t>(row) * m.cols, col0, m.cols, w);
 }
 
 template <int B>
@@ -309,11 +328,16 @@ __global__ void materialize_kernel(DevMatrix m, uint16_t* __restrict__ out, uint
     slot_coords(g, m.spr, row, grp);
     const int col0 = grp * kGroup;
     if (row >= m.rows || col0 >= m.cols) return;
-    uint16_t* dst = out + static_cast<uint64_t>(row) * m.cols;
+    uint32_t w[16];
     if constexpr (B == 16) {
-        const uint16_t* src = m.w16 + g * kGroup;
-        for (int i = 0; i < kGroup; ++i) {
-            if (col0 + i < m.cols) dst[col0 + i] = src[i];
+        const uint4* src = reinterpret_cast<const uint4*>(m.w16 + g * kGroup);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const uint4 t = src[v];
+            w[4 * v] = t.x;
+            w[4 * v + 1] = t.y;
+            w[4 * v + 2] = t.z;
+            w[4 * v + 3] = t.w;
         }
     } else {
         Raw<B> r;
@@ -321,17 +345,12 @@ __global__ void materialize_kernel(DevMatrix m, uint16_t* __restrict__ out, uint
         const float s = m.scales[row];
 #pragma unroll
         for (int d = 0; d < 8; ++d) {
-            uint32_t lo, hi, w0, w1;
+            uint32_t lo, hi;
             quad_bytes<B>(r, d, lo, hi);
-            quad_w<B>(lo, hi, s, w0, w1);
-            const uint32_t ws[4] = {w0 & 0xFFFFu, w0 >> 16, w1 & 0xFFFFu, w1 >> 16};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int col = col0 + 4 * d + j;
-                if (col < m.cols) dst[col] = static_cast<uint16_t>(ws[j]);
-            }
+            quad_w<B>(lo, hi, s, w[2 * d], w[2 * d + 1]);
         }
     }
+    store_group(out + static_cast<uint64_t>(row) * m.cols, col0, m.cols, w);
 }
 
 // ---------------------------------------------------------------------------
