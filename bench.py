@@ -41,8 +41,8 @@ MALL_BYTES = 256 << 20
 # this many elements reads exactly 2x and writes exactly 4x that many bytes.
 COPY_CAL_ELEMS = 64 << 20
 COPY_CAL_KERNEL = "float16tofloat32_copy_kernel"
-DECODE_KERNEL = "linear_decode_kernel"
-PREFILL_KERNEL = "linear_prefill_kernel"
+DECODE_KERNEL = "linear_gemv_kernel"
+PREFILL_KERNEL = "linear_prefill"          # the 256 x 256 and the 128 x 256 tile kernels
 TRAFFIC_FILE = "decode_gemv_4096x4096_b10_m1_traffic.md"
 
 
@@ -58,6 +58,8 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--prefill-steps", type=int, default=20)
     p.add_argument("--no-prefill", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--no-reference-route", action="store_true",
+                   help="skip the timings of the reference's own execution formats on this GPU")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--traffic-probe", action="store_true",
                    help="run eager GEMV/prefill launches and a calibration copy for rocprofv3 --pmc")
@@ -178,6 +180,96 @@ def bench_prefill(args) -> dict:
     return {"workload": "ElasticBit linear 4096->14336, fp16 x M=2048, threshold 0.01 (configs[3])",
             "bits": bits, "us_per_launch": round(per * 1e3, 2), "tflops": round(tflops, 2),
             "frac_fp16_mfma_peak": round(tflops / FP16_PEAK_TFLOPS, 4)}
+
+
+def read_ceiling(nbytes: int, copies: int, steps: int, warmup: int) -> dict:
+    """Best per-launch time of a kernel that only reads `nbytes` (the GEMV's
+    algorithmic bytes), over `copies` rotated buffers, launched and timed
+    exactly as the GEMV: the most any one-launch-per-step kernel over those
+    bytes reaches here.  Sweeps workgroup count and size."""
+    import ctypes
+
+    import torch
+
+    lib = ctypes.CDLL(str(ROOT / "mlbricks_amd" / "lib" / "libeb_probe_read.so"))
+    lib.eb_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int, ctypes.c_int,
+                                  ctypes.c_void_p, ctypes.c_void_p]
+    size = -(-nbytes // 16) * 16
+    bufs = [torch.empty(size, dtype=torch.uint8, device="cuda").random_(0, 255) for _ in range(copies)]
+    sink = torch.zeros(1024, dtype=torch.int32, device="cuda")
+    best = None
+    for blocks, threads in ((256, 1024), (512, 1024), (512, 512), (1024, 256), (1024, 512), (2048, 256)):
+        def mk(buf, blocks=blocks, threads=threads):
+            def launch():
+                rc = lib.eb_probe_read(buf.data_ptr(), size, blocks, threads, sink.data_ptr(),
+                                       torch.cuda.current_stream().cuda_stream)
+                if rc != 0:
+                    raise RuntimeError(f"eb_probe_read: {rc}")
+            return launch
+        try:
+            ms = time_graph([mk(b) for b in bufs], steps, warmup)
+        except RuntimeError:
+            continue
+        us = ms / steps * 1e3
+        if best is None or us < best[0]:
+            best = (us, blocks, threads)
+    us, blocks, threads = best
+    gbs = nbytes / (us * 1e-6) / 1e9
+    log(f"read ceiling: {us:.3f} us per {nbytes / 1e6:.1f} MB read ({gbs:.1f} GB/s, {blocks} x {threads})")
+    return {"us_per_launch": round(us, 3), "gbs": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "launch": f"{blocks} workgroups x {threads} threads",
+            "what": "pure-read kernel (mlbricks_amd/csrc/probe_read.hip) over the GEMV's algorithmic bytes, "
+                    "same copy rotation and graph timing"}
+
+
+def reference_route(args) -> dict:
+    """The reference's own execution formats, timed on this GPU with the same
+    methods (informational; never `value`).  Decode: at b = 9..15 the
+    reference executes W16A16 (elasticbit_runtime.cu:240-244,1174-1178), a
+    GEMV over fp16 weights, 2 bytes per weight; here that is this build's
+    GEMV kernel over b = 16 storage of the same weights.  Prefill: the
+    reference materializes fp16 weights and calls F.linear (core.py:462-471);
+    here materialize_kernel plus torch.matmul (hipBLASLt)."""
+    import torch
+
+    from mlbricks_amd.elasticbit import _native as native
+
+    out = {}
+    rows = cols = 4096
+    w = make_weight(rows, cols).float().numpy()
+    per = 2 * rows * cols
+    n_copies = max(2, -(-2 * MALL_BYTES // per) + 1)
+    mats = [native.RuntimeMatrix._compressSelected(w, 16, 0.01, 0.0) for _ in range(n_copies)]
+    x = torch.randn(1, cols, generator=torch.Generator().manual_seed(1)).half().cuda()
+    ys = [torch.empty(1, rows, dtype=torch.float16, device="cuda") for _ in mats]
+    ms = time_graph([lambda m=m, y=y: m.forwardTorch(x, out=y) for m, y in zip(mats, ys)], args.steps, args.warmup)
+    us = ms / args.steps * 1e3
+    nbytes = algorithmic_bytes(rows, cols, 16, 1)
+    out["decode_w16"] = {"us_per_launch": round(us, 3), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                         "bytes_per_launch": nbytes,
+                         "what": "configs[1] as W16A16 (fp16 weights, the reference's format at b = 9..15), "
+                                 f"{n_copies} rotated copies"}
+    log(f"reference route, decode W16: {us:.3f} us/launch ({out['decode_w16']['gbs']} GB/s on 2 B/weight)")
+    del mats, ys
+    prows, pcols, M = 14336, 4096, 2048
+    layer = compressed_layer(prows, pcols, 0.01, 512)
+    nm = layer.matrix._native
+    xp = torch.randn(M, pcols, generator=torch.Generator().manual_seed(1)).half().cuda()
+    wbuf = torch.empty(prows, pcols, dtype=torch.float16, device="cuda")
+    yp = torch.empty(M, prows, dtype=torch.float16, device="cuda")
+
+    def materialize_then_linear():
+        native.check(native.lib().eb_materialize_fp16(nm._h, wbuf.data_ptr(), native.stream_handle(wbuf.device)))
+        torch.matmul(xp, wbuf.t(), out=yp)
+
+    ms = time_graph([materialize_then_linear], args.prefill_steps, 3)
+    us = ms / args.prefill_steps * 1e3
+    flops = 2.0 * M * prows * pcols
+    out["prefill_materialize_then_linear"] = {
+        "us_per_launch": round(us, 2), "tflops": round(flops / (us * 1e-6) / 1e12, 1),
+        "what": "configs[3]: materialize_kernel to fp16, then torch.matmul (hipBLASLt), as core.py:462-471"}
+    log(f"reference route, prefill materialize + F.linear: {us:.1f} us/launch")
+    return out
 
 
 def cpu_baseline(layer, seconds: float) -> dict:
@@ -374,7 +466,9 @@ def main() -> int:
         return traffic_probe(args)
 
     g = bench_gemv(args)
+    ceiling = read_ceiling(g["bytes"], g["copies"], args.steps, args.warmup)
     prefill = None if args.no_prefill else bench_prefill(args)
+    reference = None if args.no_reference_route else reference_route(args)
     cpu = None if args.no_cpu else cpu_baseline(g["layer"], args.cpu_seconds)
     achieved = g["bytes"] / (g["per_step_ms"] * 1e-3) / 1e9
     line = {
@@ -404,9 +498,12 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic(),
+            "read_ceiling": ceiling,
+            "frac_of_read_ceiling": round(ceiling["us_per_launch"] / (g["per_step_ms"] * 1e3), 4),
         },
         "cpu_baseline": cpu,
         "prefill": prefill,
+        "reference_route": reference,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -20,6 +20,7 @@ ROOT = PKG.parent
 BUILD_DIR = HERE / "_build"
 LIB_DIR = PKG / "lib"
 LIB_NAME = "libelasticbit_hip.so"
+PROBE_LIB_NAME = "libeb_probe_read.so"
 
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 ARCH = "gfx950"
@@ -63,6 +64,10 @@ def build(verbose: bool = False) -> Path:
           f"-L{ROCM / 'lib'}", "-lamdhip64", "-lpthread"], verbose)
     out = LIB_DIR / LIB_NAME
     os.replace(tmp, out)
+    # bench.py's read-bandwidth probe, a library of its own
+    ptmp = LIB_DIR / (PROBE_LIB_NAME + ".tmp")
+    _run([hipcc, *DEVICE_FLAGS, "-shared", str(HERE / "probe_read.hip"), "-o", str(ptmp)], verbose)
+    os.replace(ptmp, LIB_DIR / PROBE_LIB_NAME)
     return out
 
 
