@@ -160,7 +160,7 @@ int eb_benchmark(eb_matrix* m, const float* x, int iterations, double* ms_per_it
 /* RuntimeMatrix.forwardTorch, runtime.cu:902-931 (decode, M = 1) and the
  * prefill route materialize + F.linear, core.py:462-471 (M > 1):
  *   y[M][rows] = x[M][cols] . W^T (+ bias), fp16 in, fp16 out, fp32 accumulate.
- * hardwareNative: b <= 10 computes fp16_rn(s_r * sum q*x); b >= 11 and
+ * hardwareNative: b <= 12 computes fp16_rn(s_r * sum q*x); b >= 13 and
  * fullPrecision compute fp16_rn(sum fp16_rn(q*s_r) * x).  bias (may be NULL)
  * is added as torch does, y = fp16_rn(y + bias).  Any M >= 1. */
 int eb_forward(const eb_matrix* m, const void* x_f16, int64_t M, void* y_f16,

@@ -578,7 +578,9 @@ struct eb_matrix {
         }
     }
 
-    bool exact_w16() const { return policy == EB_POLICY_FULL_PRECISION || bits > 10; }
+    // hardwareNative b <= 12 multiplies the integer codes (exact in fp16)
+    // and scales once; b >= 13 and fullPrecision use the decoded fp16 weights.
+    bool exact_w16() const { return policy == EB_POLICY_FULL_PRECISION || bits > 12; }
 
     int execution_width() const {
         if (bits == kFallbackBits || policy == EB_POLICY_FULL_PRECISION) return 16;

@@ -95,7 +95,7 @@ hipError_t launch_unpack(const DevMatrix& m, int16_t* out, hipStream_t stream);
 hipError_t launch_materialize(const DevMatrix& m, uint16_t* out, hipStream_t stream);
 
 // y[M][rows] = x[M][cols] . W^T (+ bias).  exact_w16 selects the decoded-fp16
-// (W16A16) arithmetic; otherwise b <= 10 uses the integer-code dot product with
+// (W16A16) arithmetic; otherwise b <= 12 uses the integer-code dot product with
 // the row scale applied once.  Requires cols % 8 == 0 and 16-byte aligned x
 // for the vector path; other shapes take the guarded scalar path.
 hipError_t launch_linear(const DevMatrix& m, bool exact_w16, const uint16_t* x, int64_t M,

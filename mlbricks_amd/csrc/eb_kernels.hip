@@ -134,20 +134,39 @@ __device__ __forceinline__ uint32_t pack_h2(_Float16 a, _Float16 b) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
-// Exact fp16 codes q for one quad, b <= 10: the byte lanes become the
-// mantissa of 1024 + u (fp16 0x6400 | u), then 1024 + qmax is subtracted.
+// Exact fp16 codes q for one quad, b <= 12 (every |q| <= 2047 is an fp16
+// integer).  The low ten bits of u become the mantissa of 1024 + u_lo
+// (fp16 0x6400 | u_lo).  For b <= 10 that is all of u, and 1024 + qmax is
+// subtracted.  For b = 11, 12 the subtraction is 2047 = 1024 + 1023, and the
+// top bits t = u >> 10 add 1024 t + 1023 - qmax, looked up with one
+// v_perm_b32 as fp16 high bytes (the low bytes are zero): b = 11, t in
+// {0, 1}: {0, 1024}; b = 12, t in {0..3}: {-1024, 0, 1024, 2048}.  Every
+// partial result is an integer of magnitude at most 2048, so each fp16 step
+// is exact.
 template <int B>
 __device__ __forceinline__ void quad_q(uint32_t lo, uint32_t hi, uint32_t& w0, uint32_t& w1) {
-    static_assert(B <= 10, "fp16 mantissa holds at most 10 code bits");
-    // hi holds only bits the byte mask 0x03030303 (or narrower) keeps, so
-    // OR-ing in the exponent byte 0x64 is a bit-field insert.
-    const uint32_t H = hi | 0x64646464u;
+    static_assert(B <= 12, "fp16 holds the codes exactly only up to 12 bits");
+    // the low two bits of each hi byte are bits 8..9 of u; OR-ing in the
+    // exponent byte 0x64 is then a bit-field insert
+    const uint32_t H = (B <= 10 ? hi : (hi & 0x03030303u)) | 0x64646464u;
     const uint32_t a = __builtin_amdgcn_perm(H, lo, 0x05010400u);  // [lo0 H0 lo1 H1]
     const uint32_t b = __builtin_amdgcn_perm(H, lo, 0x07030602u);  // [lo2 H2 lo3 H3]
-    constexpr _Float16 off = static_cast<_Float16>(1024 + Planes<B>::qmax);
+    constexpr _Float16 off = static_cast<_Float16>(B <= 10 ? 1024 + Planes<B>::qmax : 2047);
     const half2v o = {off, off};
-    w0 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, a) - o);
-    w1 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, b) - o);
+    half2v q01 = __builtin_bit_cast(half2v, a) - o;
+    half2v q23 = __builtin_bit_cast(half2v, b) - o;
+    if constexpr (B > 10) {
+        // fp16 high bytes of 1024 t + 1023 - qmax for t = 0..3
+        constexpr uint32_t lut = B == 11 ? 0x00006400u : 0x686400E4u;
+        const uint32_t t = (hi >> 2) & (B == 11 ? 0x01010101u : 0x03030303u);
+        const uint32_t tb = __builtin_amdgcn_perm(0u, lut, t);                   // [L(t0) L(t1) L(t2) L(t3)]
+        const uint32_t h01 = __builtin_amdgcn_perm(0u, tb, 0x01040004u);         // [0 L(t0) 0 L(t1)]
+        const uint32_t h23 = __builtin_amdgcn_perm(0u, tb, 0x03040204u);         // [0 L(t2) 0 L(t3)]
+        q01 = q01 + __builtin_bit_cast(half2v, h01);
+        q23 = q23 + __builtin_bit_cast(half2v, h23);
+    }
+    w0 = __builtin_bit_cast(uint32_t, q01);
+    w1 = __builtin_bit_cast(uint32_t, q23);
 }
 
 // a * b rounded to fp32.  The reference rounds products to fp32 before the
@@ -1839,7 +1858,7 @@ template <int B>
 struct LinearOp {
     static hipError_t run(const DevMatrix& m, bool exact_w16, const uint16_t* x, int64_t M, uint16_t* y,
                           const uint16_t* bias, int xvec, hipStream_t s) {
-        if constexpr (B <= 10) {
+        if constexpr (B <= 12) {
             if (!exact_w16) return run_linear_mode<B, kModeQ>(m, x, M, y, bias, xvec, s);
         }
         return run_linear_mode<B, kModeW>(m, x, M, y, bias, xvec, s);

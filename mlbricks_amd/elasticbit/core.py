@@ -9,9 +9,10 @@ canonical MLB4 bitstream with one fp32 scale per row.
 Execution on gfx950 reads the b-bit codes directly -- re-laid out at load time
 as bit planes, still b bits per weight -- and decodes them in registers:
 
-* ``hardwareNative``: b <= 10 multiplies the exact integer codes by fp16
-  activations and applies the row scale once; b >= 11 uses the decoded fp16
-  weights fp16_rn(q*s) (W16A16 arithmetic, as the reference does for b >= 9);
+* ``hardwareNative``: b <= 12 multiplies the exact integer codes (every
+  |q| <= 2047 is an fp16 integer) by fp16 activations and applies the row
+  scale once; b >= 13 uses the decoded fp16 weights fp16_rn(q*s) (W16A16
+  arithmetic, as the reference does for b >= 9);
 * ``fullPrecision``: every width uses the decoded fp16 weights;
 * one fused kernel family serves decode (M <= 16) and prefill (M > 16) on the
   matrix cores; activations stay fp16 everywhere.
