@@ -457,12 +457,16 @@ __device__ __forceinline__ void wait_vmcnt() {
 // issue order, so every activation load is issued before the weight loads
 // it must not wait behind.
 //
-// XLDS: the activations (M x K, zero-padded to whole tiles) are staged once
-// per workgroup in LDS, when they fit in kXLdsBytes; otherwise each lane with
-// an activation row loads its A operand from global memory per step.
+// XL: the activations (M x K, zero-padded to whole tiles) are staged once
+// per workgroup in LDS.  XL = 1: up to kXLdsBytes, global -> LDS directly
+// when x's rows are whole tiles and 16-byte aligned, through registers
+// (zero-padded) otherwise.  XL = 2: up to kXLdsDirectBytes, direct only, so
+// no registers are held for it.  XL = 0: each lane with an activation row
+// loads its A operand from global memory per step.
 // ---------------------------------------------------------------------------
 
 constexpr int kXLdsBytes = 32768;
+constexpr int kXLdsDirectBytes = 147456;   // 16 rows of 4608 halves
 
 // One group's weight bits as held in registers between load and decode.
 template <int B, int MODE>
@@ -535,7 +539,7 @@ __device__ __forceinline__ void decode_load_batch(const DevMatrix& m, Bits (&bit
 
 // Activation operands of one workgroup batch (steps base + wave*GPL + j):
 // from the LDS copy, or from global memory, zero past the last step.
-template <int GPL, bool XLDS>
+template <int GPL, int XL>
 __device__ __forceinline__ void decode_activations(half8 (&a)[GPL][4], const DevMatrix& m, int base, int wave,
                                                    int quarter, bool m_ok, int steps,
                                                    const uint16_t* __restrict__ xrow, const uint16_t* xsrow,
@@ -545,7 +549,7 @@ __device__ __forceinline__ void decode_activations(half8 (&a)[GPL][4], const Dev
     for (int j = 0; j < GPL; ++j) {
         const int k0 = ((first + j) * kTileGroups + quarter) * kGroup;
         const bool ok = m_ok && first + j < steps;
-        if constexpr (XLDS) {
+        if constexpr (XL != 0) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 a[j][t] = ok ? *reinterpret_cast<const half8*>(xsrow + k0 + 8 * t) : half8{0, 0, 0, 0, 0, 0, 0, 0};
@@ -577,17 +581,18 @@ __device__ __forceinline__ void decode_mul_batch(const Bits (&cur)[GPL], const h
     }
 }
 
-template <int B, int MODE, int WAVES, int GPL, bool XLDS>
+template <int B, int MODE, int WAVES, int GPL, int XL>
 __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
     DevMatrix m, const uint16_t* __restrict__ x, int M, uint16_t* __restrict__ y,
     const uint16_t* __restrict__ bias, int xvec) {
     using Bits = GroupBits<B, MODE>;
     constexpr int kThreads = 64 * WAVES;
     constexpr int kBatch = WAVES * GPL;              // steps per workgroup batch
-    constexpr int kXVecs = kXLdsBytes / 16 / kThreads;
+    constexpr int kXVecs = kXLdsBytes / 16 / kThreads;                              // XL = 1
+    constexpr int kXDirect = (XL == 2 ? kXLdsDirectBytes : kXLdsBytes) / 16 / kThreads;
     static_assert(kXVecs >= 1, "LDS activation staging needs one uint4 per thread");
     static_assert(kThreads >= 256, "the epilogue stores the 16x16 tile with one thread per element");
-    extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   // [M][spr * 128], XLDS only
+    extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   // [M][spr * 128], XL > 0 only
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -612,16 +617,17 @@ __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
     // Slot of this lane in the row tile's first tile; step st adds st * 64.
     const size_t slot0 = static_cast<size_t>(blockIdx.x) * steps * kTileSlots + lane;
 
-    uint4 xv[XLDS ? kXVecs : 1];
+    uint4 xv[XL == 1 ? kXVecs : 1];
     const int vpr = kpad / 8;                        // uint4 vectors per staged row
     // xvec == 2: rows are whole tiles wide (cols == kpad) and x is 16-byte
     // aligned, so the staged copy is x itself and goes global -> LDS
     // directly, without registers; otherwise through registers, zero-padded.
-    const bool xdirect = xvec == 2;
-    if constexpr (XLDS) {
+    // XL = 2 is launched for xvec == 2 only.
+    const bool xdirect = XL == 2 || xvec == 2;
+    if constexpr (XL != 0) {
         if (xdirect) {
 #pragma unroll
-            for (int r = 0; r < kXVecs; ++r) {
+            for (int r = 0; r < kXDirect; ++r) {
                 const int i = threadIdx.x + r * kThreads;
                 if (i < M * vpr) {
                     __builtin_amdgcn_global_load_lds(x + 8 * i,
@@ -629,7 +635,7 @@ __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
                                                      16, 0, 0);
                 }
             }
-        } else {
+        } else if constexpr (XL == 1) {
 #pragma unroll
             for (int r = 0; r < kXVecs; ++r) {
                 const int i = threadIdx.x + r * kThreads;
@@ -661,12 +667,12 @@ __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
     // MI355X: one tile per wave plus the prefetch keeps ~40 KB per CU in
     // flight, which already covers the loaded HBM latency.
     decode_load_batch<GPL>(m, buf0, slot0, wave * GPL, steps);
-    if constexpr (XLDS) {
+    if constexpr (XL != 0) {
         if (xdirect) {
             // the activation loads precede the weight loads just issued
             wait_vmcnt<GPL * GroupLoads<B, MODE>::value>();
             barrier_after_wait();
-        } else {
+        } else if constexpr (XL == 1) {
 #pragma unroll
             for (int r = 0; r < kXVecs; ++r) {
                 const int i = threadIdx.x + r * kThreads;
@@ -676,7 +682,7 @@ __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
         }
     }
     auto batch = [&](const Bits (&cur)[GPL], Bits (&nxt)[GPL], bool prefetch, int bi) {
-        decode_activations<GPL, XLDS>(a, m, bi * kBatch, wave, quarter, m_ok, steps, xrow, xsrow, xvec);
+        decode_activations<GPL, XL>(a, m, bi * kBatch, wave, quarter, m_ok, steps, xrow, xsrow, xvec);
         if (prefetch) decode_load_batch<GPL>(m, nxt, slot0, (bi + 1) * kBatch + wave * GPL, steps);
         decode_mul_batch<B, MODE, GPL>(cur, a, bi * kBatch + wave * GPL, steps, s, acc);
     };
@@ -1799,10 +1805,13 @@ hipError_t run_linear_mode(const DevMatrix& m, const uint16_t* x, int64_t M, uin
     } else if (M <= kDecodeMaxM) {
         const size_t xbytes = static_cast<size_t>(M) * m.spr * kTileGroups * kGroup * 2;
         if (xbytes <= static_cast<size_t>(kXLdsBytes)) {
-            hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, true>), dim3(m.rtiles),
+            hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, 1>), dim3(m.rtiles),
+                               dim3(64 * kDecodeWaves), xbytes, s, m, x, static_cast<int>(M), y, bias, xvec);
+        } else if (xvec == 2 && xbytes <= static_cast<size_t>(kXLdsDirectBytes)) {
+            hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, 2>), dim3(m.rtiles),
                                dim3(64 * kDecodeWaves), xbytes, s, m, x, static_cast<int>(M), y, bias, xvec);
         } else {
-            hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, false>), dim3(m.rtiles),
+            hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, 0>), dim3(m.rtiles),
                                dim3(64 * kDecodeWaves), 0, s, m, x, static_cast<int>(M), y, bias, xvec);
         }
     } else if (MODE != kModeRaw && B <= 10 && EBK_PREFILL_WIDE && xvec && M >= kWRows && m.rows >= kWN &&

@@ -209,6 +209,35 @@ def test_forward_ragged_shapes(native, b, rows, cols, M):
     assert _rel_max(y, ref) <= TOL
 
 
+@pytest.mark.parametrize("M", [2, 4, 8, 16])
+@pytest.mark.parametrize("cols,aligned", [(4096, True), (4608, True), (11008, True), (1000, True), (4096, False)])
+@pytest.mark.parametrize("b", [8, 10, 13])
+def test_decode_activation_staging(native, M, cols, aligned, b):
+    """M <= 16 decode over the three activation paths: staged in LDS up to
+    32 KB (direct or through registers), staged directly up to 144 KB (16 x
+    4608 exactly) when x rows are whole 128-column tiles and 16-byte aligned,
+    read per lane from global memory otherwise -- with ragged K and an
+    unaligned x."""
+    rows = 40
+    rng = np.random.default_rng(M * 31 + cols + b)
+    q = _codes(rng, rows, cols, b)
+    s = rng.uniform(0.002, 0.05, size=rows).astype(np.float32)
+    m = native.RuntimeMatrix._compressSelectedCodes(q, s, b, 0.01, 0.0)
+    x0 = _x16(rng, M, cols)
+    if aligned:
+        x = x0
+    else:
+        buf = torch.empty(M * cols + 1, dtype=torch.float16, device="cuda")
+        x = buf[1:].view(M, cols)
+        x.copy_(x0)
+        assert x.data_ptr() % 16 != 0
+    y = m.forwardTorch(x).float().cpu().numpy()
+    payload = ora.pack_codes(q, b)
+    ref = _reference(payload, s, rows, cols, b, x.cpu().numpy().view(np.uint16))
+    assert _rel_max(y, ref) <= TOL
+    _check_reference_w16(y, payload, s, rows, cols, b, x.cpu().numpy().view(np.uint16))
+
+
 @pytest.mark.parametrize("M", [1, 24])
 def test_forward_unaligned_activation_pointer(native, M):
     rows, cols, b = 40, 256, 10
