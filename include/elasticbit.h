@@ -166,6 +166,17 @@ int eb_benchmark(eb_matrix* m, const float* x, int iterations, double* ms_per_it
 int eb_forward(const eb_matrix* m, const void* x_f16, int64_t M, void* y_f16,
                const void* bias_f16, void* stream);
 
+/* Several matrices that read the same activations (no single-call
+ * counterpart in the reference: Stage-2F concatenates the materialized fp16
+ * weights of Q/K/V and Gate/Up and runs one F.linear, stage2f.py:382-420):
+ *   ys[j][M][rows_j] = x[M][cols] . W_j^T (+ biases[j]),  j < count,
+ * each as eb_forward computes it.  Every matrix has the same cols and lives
+ * on one device; biases may be NULL, as may any biases[j].  For M <= 16,
+ * consecutive matrices of one width and policy (up to four) share one
+ * launch, so the decode of a QKV or Gate/Up group pays one launch. */
+int eb_forward_multi(const eb_matrix* const* ms, int count, const void* x_f16, int64_t M,
+                     void* const* ys_f16, const void* const* biases_f16, void* stream);
+
 /* RuntimeMatrix._materializeTorch, runtime.cu:982-1022: out [rows][cols] fp16
  * = fp16_rn(q*s) (b = 16: the stored fp16). */
 int eb_materialize_fp16(const eb_matrix* m, void* out_f16, void* stream);

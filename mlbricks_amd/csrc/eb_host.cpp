@@ -929,6 +929,40 @@ int eb_forward(const eb_matrix* m, const void* x_f16, int64_t M, void* y_f16, co
     });
 }
 
+int eb_forward_multi(const eb_matrix* const* ms, int count, const void* x_f16, int64_t M, void* const* ys_f16,
+                     const void* const* biases_f16, void* stream) {
+    return guarded([&] {
+        require(ms && ys_f16 && x_f16, "forward_multi: null pointer");
+        require(count >= 1, "forward_multi: count must be positive");
+        require(M >= 1 && M <= 0x7fffffffLL, "forward: M must be in [1, 2^31)");
+        for (int j = 0; j < count; ++j) {
+            require(ms[j] && ys_f16[j], "forward_multi: null pointer");
+            ms[j]->require_device();
+            require(ms[j]->cols == ms[0]->cols, "forward_multi: matrices must share in_features");
+            require(ms[j]->device == ms[0]->device, "forward_multi: matrices must be on one device");
+        }
+        DeviceGuard guard(ms[0]->device);
+        // consecutive matrices of one width and arithmetic share a launch
+        ebk::DevMatrix dev[ebk::kMultiMax];
+        uint16_t* ys[ebk::kMultiMax];
+        const uint16_t* bs[ebk::kMultiMax];
+        for (int j0 = 0; j0 < count;) {
+            const bool w16 = ms[j0]->exact_w16();
+            int n = 0;
+            while (j0 + n < count && n < ebk::kMultiMax && ms[j0 + n]->bits == ms[j0]->bits &&
+                   ms[j0 + n]->exact_w16() == w16) {
+                dev[n] = ms[j0 + n]->dev;
+                ys[n] = static_cast<uint16_t*>(ys_f16[j0 + n]);
+                bs[n] = biases_f16 ? static_cast<const uint16_t*>(biases_f16[j0 + n]) : nullptr;
+                ++n;
+            }
+            EB_HIP(ebk::launch_linear_multi(dev, n, w16, static_cast<const uint16_t*>(x_f16), M, ys, bs,
+                                            static_cast<hipStream_t>(stream)));
+            j0 += n;
+        }
+    });
+}
+
 int eb_materialize_fp16(const eb_matrix* m, void* out_f16, void* stream) {
     return guarded([&] {                                 // runtime.cu:982-1022
         require(m && out_f16, "materialize: null pointer");

@@ -101,6 +101,24 @@ hipError_t launch_materialize(const DevMatrix& m, uint16_t* out, hipStream_t str
 hipError_t launch_linear(const DevMatrix& m, bool exact_w16, const uint16_t* x, int64_t M,
                          uint16_t* y, const uint16_t* bias, hipStream_t stream);
 
+// Several matrices that read the same x in one decode launch (M <= 16):
+// matrix j owns the grid's row tiles [tile0[j-1], tile0[j]) and writes its
+// own y.  Matrix 0 is the launch's own argument; this holds the others.
+constexpr int kMultiMax = 4;
+struct MultiTail {
+    DevMatrix m[kMultiMax - 1];               // matrices 1 .. count - 1
+    uint16_t* y[kMultiMax - 1] = {};
+    const uint16_t* bias[kMultiMax - 1] = {};
+    int tile0[kMultiMax - 1] = {};            // first grid row tile of matrix j + 1
+    int count = 1;                            // matrices in the launch
+};
+
+// ys[j][M][ms[j].rows] = x[M][cols] . W_j^T (+ biases[j]) for count <= kMultiMax
+// matrices with the same cols, bits and arithmetic: one launch when
+// M <= 16, one launch per matrix otherwise.  biases may be null.
+hipError_t launch_linear_multi(const DevMatrix* ms, int count, bool exact_w16, const uint16_t* x, int64_t M,
+                               uint16_t* const* ys, const uint16_t* const* biases, hipStream_t stream);
+
 // Prefill tile shape: 0 auto, 1 128 x 256, 2 256 x 256 (process-wide).
 void set_prefill_tiles(int mode);
 

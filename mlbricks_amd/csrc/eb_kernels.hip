@@ -581,10 +581,31 @@ __device__ __forceinline__ void decode_mul_batch(const Bits (&cur)[GPL], const h
     }
 }
 
+// The matrix, row tile, output and bias of this workgroup in a launch over
+// several matrices (MultiTail); a single-matrix launch keeps its arguments.
+__device__ __forceinline__ int select_matrix(const MultiTail& mt, DevMatrix& m, uint16_t* __restrict__& y,
+                                             const uint16_t* __restrict__& bias) {
+    int tile = blockIdx.x;
+    if (mt.count > 1) {
+        int base = 0;
+#pragma unroll
+        for (int j = 0; j < kMultiMax - 1; ++j) {
+            if (j + 1 < mt.count && tile >= mt.tile0[j]) {
+                m = mt.m[j];
+                y = mt.y[j];
+                bias = mt.bias[j];
+                base = mt.tile0[j];
+            }
+        }
+        tile -= base;
+    }
+    return tile;
+}
+
 template <int B, int MODE, int WAVES, int GPL, int XL>
 __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
     DevMatrix m, const uint16_t* __restrict__ x, int M, uint16_t* __restrict__ y,
-    const uint16_t* __restrict__ bias, int xvec) {
+    const uint16_t* __restrict__ bias, int xvec, const MultiTail mt) {
     using Bits = GroupBits<B, MODE>;
     constexpr int kThreads = 64 * WAVES;
     constexpr int kBatch = WAVES * GPL;              // steps per workgroup batch
@@ -594,11 +615,12 @@ __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
     static_assert(kThreads >= 256, "the epilogue stores the 16x16 tile with one thread per element");
     extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   // [M][spr * 128], XL > 0 only
 
+    const int tile = select_matrix(mt, m, y, bias);
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int nl = lane & 15;
     const int quarter = lane >> 4;
-    const int row = blockIdx.x * kTileRows + nl;
+    const int row = tile * kTileRows + nl;
     const bool m_ok = nl < M;                        // activation row of the A operand
     const int steps = m.spr;
     const int kpad = steps * kTileGroups * kGroup;
@@ -607,7 +629,7 @@ __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
     // Thread o < 256 stores output (4*(o%64/16) + o/64, n0 + o%16) at the end;
     // its row scale and bias are loaded now, ahead of the weights, so that
     // the epilogue does not wait for another memory round trip.
-    const int on = blockIdx.x * kTileRows + (threadIdx.x & 15);
+    const int on = tile * kTileRows + (threadIdx.x & 15);
     float out_scale = 1.0f;
     uint16_t out_bias = 0;
     if (threadIdx.x < 256 && on < m.rows) {
@@ -615,7 +637,7 @@ __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
         if (bias) out_bias = bias[on];
     }
     // Slot of this lane in the row tile's first tile; step st adds st * 64.
-    const size_t slot0 = static_cast<size_t>(blockIdx.x) * steps * kTileSlots + lane;
+    const size_t slot0 = static_cast<size_t>(tile) * steps * kTileSlots + lane;
 
     uint4 xv[XL == 1 ? kXVecs : 1];
     const int vpr = kpad / 8;                        // uint4 vectors per staged row
@@ -738,17 +760,19 @@ constexpr int kGemvMaxSteps = 2 * kGemvWaves;
 
 template <int B, int MODE>
 __global__ __launch_bounds__(64 * kGemvWaves) void linear_gemv_kernel(
-    DevMatrix m, const uint16_t* __restrict__ x, uint16_t* __restrict__ y, const uint16_t* __restrict__ bias) {
+    DevMatrix m, const uint16_t* __restrict__ x, uint16_t* __restrict__ y, const uint16_t* __restrict__ bias,
+    const MultiTail mt) {
     using Bits = GroupBits<B, MODE>;
     extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   // [cols], cols % 128 == 0
     __shared__ float red[kGemvWaves][kTileRows];
 
+    const int tile = select_matrix(mt, m, y, bias);
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int nl = lane & 15;
     const int quarter = lane >> 4;
     const int steps = m.spr;
-    const int row = blockIdx.x * kTileRows + nl;
+    const int row = tile * kTileRows + nl;
     float s = 0.0f;
     if constexpr (MODE == kModeW) s = row < m.rows ? m.scales[row] : 0.0f;
     float out_scale = 1.0f;
@@ -763,7 +787,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void linear_gemv_kernel(
         __builtin_amdgcn_global_load_lds(x + 8 * threadIdx.x, (lds_void_ptr)(xs + 8 * (threadIdx.x & ~63u)), 16, 0,
                                          0);
     }
-    const size_t slot0 = static_cast<size_t>(blockIdx.x) * steps * kTileSlots + lane;
+    const size_t slot0 = static_cast<size_t>(tile) * steps * kTileSlots + lane;
     Bits b0, b1;
     b0.load(m, slot0 + static_cast<size_t>(min(wave, steps - 1)) * kTileSlots);
     b1.load(m, slot0 + static_cast<size_t>(min(wave + kGemvWaves, steps - 1)) * kTileSlots);
@@ -1796,24 +1820,29 @@ inline bool prefer_wide_tiles(int64_t M, int rows, int cus) {
     return t_wide < t_narrow;
 }
 
+// mt: the other matrices of a multi-matrix decode launch (count 1 for a
+// single matrix; only M <= kDecodeMaxM takes more than one).
 template <int B, int MODE>
 hipError_t run_linear_mode(const DevMatrix& m, const uint16_t* x, int64_t M, uint16_t* y,
-                           const uint16_t* bias, int xvec, hipStream_t s) {
+                           const uint16_t* bias, int xvec, hipStream_t s, const MultiTail& mt) {
+    const int tiles = mt.count > 1 ? mt.tile0[mt.count - 2] + mt.m[mt.count - 2].rtiles : m.rtiles;
     if (M == 1 && xvec == 2 && m.spr <= kGemvMaxSteps && ((EBK_GEMV_MODES >> MODE) & 1)) {
-        hipLaunchKernelGGL((linear_gemv_kernel<B, MODE>), dim3(m.rtiles), dim3(64 * kGemvWaves),
-                           static_cast<size_t>(m.cols) * 2, s, m, x, y, bias);
+        hipLaunchKernelGGL((linear_gemv_kernel<B, MODE>), dim3(tiles), dim3(64 * kGemvWaves),
+                           static_cast<size_t>(m.cols) * 2, s, m, x, y, bias, mt);
     } else if (M <= kDecodeMaxM) {
         const size_t xbytes = static_cast<size_t>(M) * m.spr * kTileGroups * kGroup * 2;
         if (xbytes <= static_cast<size_t>(kXLdsBytes)) {
-            hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, 1>), dim3(m.rtiles),
-                               dim3(64 * kDecodeWaves), xbytes, s, m, x, static_cast<int>(M), y, bias, xvec);
+            hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, 1>), dim3(tiles),
+                               dim3(64 * kDecodeWaves), xbytes, s, m, x, static_cast<int>(M), y, bias, xvec, mt);
         } else if (xvec == 2 && xbytes <= static_cast<size_t>(kXLdsDirectBytes)) {
-            hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, 2>), dim3(m.rtiles),
-                               dim3(64 * kDecodeWaves), xbytes, s, m, x, static_cast<int>(M), y, bias, xvec);
+            hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, 2>), dim3(tiles),
+                               dim3(64 * kDecodeWaves), xbytes, s, m, x, static_cast<int>(M), y, bias, xvec, mt);
         } else {
-            hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, 0>), dim3(m.rtiles),
-                               dim3(64 * kDecodeWaves), 0, s, m, x, static_cast<int>(M), y, bias, xvec);
+            hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, 0>), dim3(tiles),
+                               dim3(64 * kDecodeWaves), 0, s, m, x, static_cast<int>(M), y, bias, xvec, mt);
         }
+    } else if (mt.count > 1) {
+        return hipErrorInvalidValue;      // the launcher splits prefill per matrix
     } else if (MODE != kModeRaw && B <= 10 && EBK_PREFILL_WIDE && xvec && M >= kWRows && m.rows >= kWN &&
                static_cast<uint64_t>(M) * m.cols * 2 < (uint64_t(1) << 32) &&
                prefer_wide_tiles(M, m.rows, device_cu_count())) {
@@ -1866,11 +1895,11 @@ hipError_t run_linear_mode(const DevMatrix& m, const uint16_t* x, int64_t M, uin
 template <int B>
 struct LinearOp {
     static hipError_t run(const DevMatrix& m, bool exact_w16, const uint16_t* x, int64_t M, uint16_t* y,
-                          const uint16_t* bias, int xvec, hipStream_t s) {
+                          const uint16_t* bias, int xvec, hipStream_t s, const MultiTail& mt) {
         if constexpr (B <= 12) {
-            if (!exact_w16) return run_linear_mode<B, kModeQ>(m, x, M, y, bias, xvec, s);
+            if (!exact_w16) return run_linear_mode<B, kModeQ>(m, x, M, y, bias, xvec, s, mt);
         }
-        return run_linear_mode<B, kModeW>(m, x, M, y, bias, xvec, s);
+        return run_linear_mode<B, kModeW>(m, x, M, y, bias, xvec, s, mt);
     }
 };
 
@@ -1902,14 +1931,55 @@ hipError_t launch_materialize(const DevMatrix& m, uint16_t* out, hipStream_t str
     return dispatch_bits<MaterializeOp>(m.bits, m, out, stream);
 }
 
-hipError_t launch_linear(const DevMatrix& m, bool exact_w16, const uint16_t* x, int64_t M, uint16_t* y,
-                         const uint16_t* bias, hipStream_t stream) {
-    // 1: rows of x can be read 16 bytes at a time; 2: and they span whole
-    // 128-column tiles, so x needs no zero padding
+namespace {
+
+// 1: rows of x can be read 16 bytes at a time; 2: and they span whole
+// 128-column tiles, so x needs no zero padding
+int x_vector_mode(const DevMatrix& m, const uint16_t* x) {
     int xvec = (m.cols % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0);
     if (xvec && m.cols % (kTileGroups * kGroup) == 0) xvec = 2;
-    if (m.bits == 16) return run_linear_mode<8, kModeRaw>(m, x, M, y, bias, xvec, stream);
-    return dispatch_bits<LinearOp>(m.bits, m, exact_w16, x, M, y, bias, xvec, stream);
+    return xvec;
+}
+
+hipError_t run_linear(const DevMatrix& m, bool exact_w16, const uint16_t* x, int64_t M, uint16_t* y,
+                      const uint16_t* bias, hipStream_t stream, const MultiTail& mt) {
+    const int xvec = x_vector_mode(m, x);
+    if (m.bits == 16) return run_linear_mode<8, kModeRaw>(m, x, M, y, bias, xvec, stream, mt);
+    return dispatch_bits<LinearOp>(m.bits, m, exact_w16, x, M, y, bias, xvec, stream, mt);
+}
+
+}  // namespace
+
+hipError_t launch_linear(const DevMatrix& m, bool exact_w16, const uint16_t* x, int64_t M, uint16_t* y,
+                         const uint16_t* bias, hipStream_t stream) {
+    return run_linear(m, exact_w16, x, M, y, bias, stream, MultiTail{});
+}
+
+hipError_t launch_linear_multi(const DevMatrix* ms, int count, bool exact_w16, const uint16_t* x, int64_t M,
+                               uint16_t* const* ys, const uint16_t* const* biases, hipStream_t stream) {
+    if (count < 1 || count > kMultiMax) return hipErrorInvalidValue;
+    for (int j = 1; j < count; ++j) {
+        if (ms[j].cols != ms[0].cols || ms[j].bits != ms[0].bits) return hipErrorInvalidValue;
+    }
+    if (M > kDecodeMaxM) {
+        for (int j = 0; j < count; ++j) {
+            const hipError_t e = run_linear(ms[j], exact_w16, x, M, ys[j], biases ? biases[j] : nullptr, stream,
+                                            MultiTail{});
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
+    MultiTail mt;
+    mt.count = count;
+    int tile = ms[0].rtiles;
+    for (int j = 1; j < count; ++j) {
+        mt.m[j - 1] = ms[j];
+        mt.y[j - 1] = ys[j];
+        mt.bias[j - 1] = biases ? biases[j] : nullptr;
+        mt.tile0[j - 1] = tile;
+        tile += ms[j].rtiles;
+    }
+    return run_linear(ms[0], exact_w16, x, M, ys[0], biases ? biases[0] : nullptr, stream, mt);
 }
 
 hipError_t launch_packed_linear(const void* x, int x_dtype, int64_t M, const uint8_t* packed,

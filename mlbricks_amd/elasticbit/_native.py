@@ -11,7 +11,7 @@ from __future__ import annotations
 import ctypes
 import os
 from pathlib import Path
-from typing import Any
+from typing import Any, Sequence
 
 import numpy as np
 import torch
@@ -95,6 +95,7 @@ _sig("eb_dequantize_host", [_vp, _f32p])
 _sig("eb_forward_host", [_vp, _f32p, _f32p])
 _sig("eb_benchmark", [_vp, _f32p, _i, ctypes.POINTER(_d)])
 _sig("eb_forward", [_vp, _vp, _i64, _vp, _vp, _vp])
+_sig("eb_forward_multi", [_vp, _i, _vp, _i64, _vp, _vp, _vp])
 _sig("eb_materialize_fp16", [_vp, _vp, _vp])
 _sig("eb_unpack_codes", [_vp, _vp, _vp])
 _sig("eb_packed_linear", [_vp, _i, _i64, _vp, _vp, _i, _vp, _i, _i64, _i64, _i64, _vp, _vp])
@@ -199,6 +200,45 @@ def backendInfo() -> dict:
 
 
 PREFILL_TILES = {"auto": 0, "narrow": 1, "wide": 2}
+
+
+def forward_torch_multi(matrices: Sequence["RuntimeMatrix"], input: torch.Tensor,
+                        biases: Sequence[torch.Tensor | None] | None = None) -> list[torch.Tensor]:
+    """``[m.forwardTorch(input, bias=b) for m, b in zip(matrices, biases)]``
+    in as few launches as the widths allow: matrices that read the same
+    activations (a QKV or Gate/Up group) share one decode launch for up to
+    16 rows of ``input``.  Every matrix must have ``cols`` equal to the last
+    dimension of ``input`` and live on its device.  No single-call
+    counterpart in the reference, whose Stage-2F concatenates the
+    materialized weights instead (stage2f.py:382-420)."""
+    mats = list(matrices)
+    if not mats:
+        raise ValueError("forwardTorchMulti needs at least one matrix")
+    props = [m._p() for m in mats]
+    for m, p in zip(mats, props):
+        m._check_input(input, p)
+    if biases is not None and len(biases) != len(mats):
+        raise ValueError("biases must hold one entry (or None) per matrix")
+    x = input.contiguous()
+    rows_in = x.numel() // props[0].cols
+    outs = [torch.empty((*x.shape[:-1], p.rows), dtype=torch.float16, device=x.device) for p in props]
+    bs: list[torch.Tensor | None] = []
+    for j, p in enumerate(props):
+        b = None if biases is None else biases[j]
+        if b is not None:
+            if b.dtype != torch.float16 or b.numel() != p.rows or b.device != x.device:
+                raise ValueError("bias must be fp16 [rows] on the input device")
+            b = b.contiguous()
+        bs.append(b)
+    if rows_in == 0:
+        return outs
+    n = len(mats)
+    handles = (ctypes.c_void_p * n)(*[m._h for m in mats])
+    ys = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
+    bptr = (ctypes.c_void_p * n)(*[b.data_ptr() if b is not None else None for b in bs])
+    with torch.cuda.device(x.device):
+        check(_lib.eb_forward_multi(handles, n, x.data_ptr(), rows_in, ys, bptr, stream_handle(x.device)))
+    return outs
 
 
 def set_prefill_tiles(mode: str) -> None:

@@ -274,6 +274,17 @@ class RuntimeMatrix:
         values = np.asarray(x, dtype=np.float32).reshape(-1)
         return np.asarray(self._native.forward(np.ascontiguousarray(values)))
 
+    @staticmethod
+    def forwardTorchMulti(matrices: Sequence["RuntimeMatrix"], x: torch.Tensor,
+                          biases: Sequence[torch.Tensor | None] | None = None) -> list[torch.Tensor]:
+        """``[m.forward(x) (+ bias) for m in matrices]`` for matrices that read
+        the same fp16 CUDA activations, in one decode launch per run of equal
+        widths (up to four matrices, up to 16 activation rows).  No
+        single-call counterpart in the reference (its Stage-2F concatenates
+        the materialized weights, stage2f.py:382-420)."""
+        native = _requireNative()
+        return native.forward_torch_multi([m._native for m in matrices], x, biases)
+
     def benchmark(self, x: Any, iterations: int = 500) -> float:
         if torch.is_tensor(x):
             x = x.detach().float().cpu().numpy()

@@ -210,6 +210,19 @@ def test_device_calls_fail_loudly_without_device():
         m._materializeTorch()
 
 
+def test_forward_multi_validates_before_any_device_work():
+    lib = native.lib()
+    m = RM._compressSelectedCodes(np.zeros((4, 32), np.int16), np.ones(4, np.float32), 10, 0.01, 0.0)
+    handles = (ctypes.c_void_p * 2)(m._h, m._h)
+    ys = (ctypes.c_void_p * 2)(None, None)
+    assert lib.eb_forward_multi(None, 1, None, 1, None, None, None) != 0
+    assert "null pointer" in lib.eb_last_error().decode()
+    assert lib.eb_forward_multi(handles, 0, ctypes.c_void_p(16), 1, ys, None, None) != 0
+    assert "count must be positive" in lib.eb_last_error().decode()
+    assert lib.eb_forward_multi(handles, 2, ctypes.c_void_p(16), 0, ys, None, None) != 0
+    assert "M must be" in lib.eb_last_error().decode()
+
+
 def test_prefill_tile_mode_is_validated():
     with pytest.raises(ValueError, match="prefill tile mode"):
         native.set_prefill_tiles("square")

@@ -238,6 +238,82 @@ def test_decode_activation_staging(native, M, cols, aligned, b):
     _check_reference_w16(y, payload, s, rows, cols, b, x.cpu().numpy().view(np.uint16))
 
 
+# Matrix groups for the multi-matrix decode: (rows, b, policy) per matrix.
+# A GQA-style QKV group, a Gate/Up pair, five matrices (a launch of four
+# plus one), mixed widths and policies (split into runs of equal ones), and
+# the fp16 fallback.
+_MULTI_GROUPS = {
+    "qkv": [(1024, 10, "hardwareNative"), (64, 10, "hardwareNative"), (64, 10, "hardwareNative")],
+    "gateup": [(2816, 9, "hardwareNative"), (2816, 9, "hardwareNative")],
+    "five": [(48, 8, "hardwareNative")] * 5,
+    "mixed": [(100, 10, "hardwareNative"), (40, 8, "hardwareNative"), (70, 10, "hardwareNative"),
+              (70, 10, "fullPrecision"), (33, 13, "hardwareNative"), (50, 10, "hardwareNative")],
+    "fp16": [(64, 16, "hardwareNative"), (80, 16, "hardwareNative")],
+}
+
+
+@pytest.mark.parametrize("group", sorted(_MULTI_GROUPS))
+@pytest.mark.parametrize("M", [1, 3, 16, 20])
+@pytest.mark.parametrize("cols,aligned", [(1024, True), (1000, True), (512, False)])
+def test_forward_multi_matches_single_forwards(native, group, M, cols, aligned):
+    """forward_torch_multi returns, bit for bit, what each matrix's own
+    forwardTorch returns (one shared decode launch per run of equal widths
+    for M <= 16, one launch per matrix above), with and without biases; the
+    first matrix is also checked against the fp64 oracle."""
+    rng = np.random.default_rng(M * 7 + cols + len(group))
+    mats, codes, scales = [], [], []
+    for rows, b, policy in _MULTI_GROUPS[group]:
+        if b == 16:
+            w = (rng.standard_normal((rows, cols)) * 0.05).astype(np.float32)
+            mats.append(native.RuntimeMatrix._compressSelected(w, 16, 0.01, 0.0, policy))
+            codes.append(None)
+            scales.append(None)
+            continue
+        q = _codes(rng, rows, cols, b)
+        s = rng.uniform(0.002, 0.05, size=rows).astype(np.float32)
+        mats.append(native.RuntimeMatrix._compressSelectedCodes(q, s, b, 0.01, 0.0, policy))
+        codes.append(q)
+        scales.append(s)
+    x0 = _x16(rng, M, cols)
+    if aligned:
+        x = x0
+    else:
+        buf = torch.empty(M * cols + 1, dtype=torch.float16, device="cuda")
+        x = buf[1:].view(M, cols)
+        x.copy_(x0)
+    biases = [None if j % 2 else torch.from_numpy(rng.standard_normal(m.rows).astype(np.float16)).cuda()
+              for j, m in enumerate(mats)]
+    for bs in (None, biases):
+        ys = native.forward_torch_multi(mats, x, bs)
+        assert len(ys) == len(mats)
+        for j, (m, y) in enumerate(zip(mats, ys)):
+            single = m.forwardTorch(x, bias=None if bs is None else bs[j])
+            assert y.shape == (M, m.rows)
+            assert torch.equal(y, single), f"matrix {j} of {group}"
+    if codes[0] is not None:
+        rows, b, policy = _MULTI_GROUPS[group][0]
+        ref = _reference(ora.pack_codes(codes[0], b), scales[0], rows, cols, b,
+                         x.cpu().numpy().view(np.uint16), policy)
+        y0 = native.forward_torch_multi(mats, x)[0]
+        assert _rel_max(y0.float().cpu().numpy(), ref) <= TOL
+
+
+def test_forward_multi_rejects_mismatched_inputs(native):
+    rng = np.random.default_rng(5)
+    a = native.RuntimeMatrix._compressSelectedCodes(_codes(rng, 32, 256, 10), np.ones(32, np.float32), 10, 0.01, 0.0)
+    b = native.RuntimeMatrix._compressSelectedCodes(_codes(rng, 32, 128, 10), np.ones(32, np.float32), 10, 0.01, 0.0)
+    x = _x16(rng, 1, 256)
+    with pytest.raises(ValueError, match="last dimension equals cols"):
+        native.forward_torch_multi([a, b], x)
+    with pytest.raises(ValueError, match="at least one matrix"):
+        native.forward_torch_multi([], x)
+    with pytest.raises(ValueError, match="one entry"):
+        native.forward_torch_multi([a, a], x, [None])
+    lib = native.lib()
+    assert lib.eb_forward_multi(None, 1, x.data_ptr(), 1, None, None, None) != 0
+    assert "null pointer" in lib.eb_last_error().decode()
+
+
 @pytest.mark.parametrize("M", [1, 24])
 def test_forward_unaligned_activation_pointer(native, M):
     rows, cols, b = 40, 256, 10
