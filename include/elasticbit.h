@@ -177,6 +177,21 @@ int eb_forward(const eb_matrix* m, const void* x_f16, int64_t M, void* y_f16,
 int eb_forward_multi(const eb_matrix* const* ms, int count, const void* x_f16, int64_t M,
                      void* const* ys_f16, const void* const* biases_f16, void* stream);
 
+/* The GPU width search of ElasticBit.compress (_selectBitsTorch,
+ * core.py:112-195) fused into one pass over the weights.  For fp16 weights
+ * w [rows][cols] and up to EB_ANALYZE_MAX_SAMPLES fp16 calibration rows
+ * x [samples][cols] (device pointers), with max_abs[r] = max_c |w[r][c]|
+ * (fp32, device), it writes partials [ceil(rows / EB_ANALYZE_TILE_ROWS)]
+ * [EB_ANALYZE_SUMS] (fp32, device): per tile of weight rows, sum |ref|^2,
+ * then sum |full_b - ref|^2 for b = 3..15, then sum |hw_b - ref|^2 for
+ * b = 3..8, where ref = fp16(x . w^T), full_b = fp16(x . fp16(q_b s_b)^T) and
+ * hw_b = fp16((x . q_b^T) s_b).  The tiles' sums give the reference's relL2
+ * errors (core.py:103-108); more calibration rows are more calls.  Stream-
+ * ordered, allocates nothing. */
+enum { EB_ANALYZE_TILE_ROWS = 16, EB_ANALYZE_MAX_SAMPLES = 32, EB_ANALYZE_SUMS = 20 };
+int eb_analyze_widths_device(const void* w_f16, int64_t rows, int64_t cols, const void* x_f16, int64_t samples,
+                             const float* max_abs, float* partials, void* stream);
+
 /* RuntimeMatrix._materializeTorch, runtime.cu:982-1022: out [rows][cols] fp16
  * = fp16_rn(q*s) (b = 16: the stored fp16). */
 int eb_materialize_fp16(const eb_matrix* m, void* out_f16, void* stream);

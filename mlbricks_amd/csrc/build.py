@@ -56,11 +56,13 @@ def build(verbose: bool = False) -> Path:
     LIB_DIR.mkdir(exist_ok=True)
     inc = [f"-I{ROOT / 'include'}", f"-I{HERE}", f"-I{ROCM / 'include'}"]
     kobj = BUILD_DIR / "eb_kernels.o"
+    aobj = BUILD_DIR / "eb_analyze.o"
     hobj = BUILD_DIR / "eb_host.o"
     _run([hipcc, *DEVICE_FLAGS, *inc, "-c", str(HERE / "eb_kernels.hip"), "-o", str(kobj)], verbose)
+    _run([hipcc, *DEVICE_FLAGS, *inc, "-c", str(HERE / "eb_analyze.hip"), "-o", str(aobj)], verbose)
     _run([clangxx, *HOST_FLAGS, *inc, "-c", str(HERE / "eb_host.cpp"), "-o", str(hobj)], verbose)
     tmp = LIB_DIR / (LIB_NAME + ".tmp")
-    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), str(kobj), str(hobj),
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), str(kobj), str(aobj), str(hobj),
           f"-L{ROCM / 'lib'}", "-lamdhip64", "-lpthread"], verbose)
     out = LIB_DIR / LIB_NAME
     os.replace(tmp, out)

@@ -963,6 +963,24 @@ int eb_forward_multi(const eb_matrix* const* ms, int count, const void* x_f16, i
     });
 }
 
+int eb_analyze_widths_device(const void* w_f16, int64_t rows, int64_t cols, const void* x_f16, int64_t samples,
+                             const float* max_abs, float* partials, void* stream) {
+    return guarded([&] {                                 // core.py:112-195
+        static_assert(EB_ANALYZE_TILE_ROWS == ebk::kAnalyzeTileRows && EB_ANALYZE_SUMS == ebk::kAnalyzeSums &&
+                          EB_ANALYZE_MAX_SAMPLES == ebk::kAnalyzeMaxSamples,
+                      "analyzer constants");
+        require(w_f16 && x_f16 && max_abs && partials, "analyze_widths: null pointer");
+        require(rows >= 1 && cols >= 1 && rows <= 0x7fffffffLL && cols <= 0x7fffffffLL,
+                "analyze_widths: rows and cols must be in [1, 2^31)");
+        require(samples >= 1 && samples <= EB_ANALYZE_MAX_SAMPLES,
+                "analyze_widths: samples must be in [1, 32]");
+        EB_HIP(ebk::launch_analyze_widths(static_cast<const uint16_t*>(w_f16), static_cast<int>(rows),
+                                          static_cast<int>(cols), static_cast<const uint16_t*>(x_f16),
+                                          static_cast<int>(samples), max_abs, partials,
+                                          static_cast<hipStream_t>(stream)));
+    });
+}
+
 int eb_materialize_fp16(const eb_matrix* m, void* out_f16, void* stream) {
     return guarded([&] {                                 // runtime.cu:982-1022
         require(m && out_f16, "materialize: null pointer");

@@ -119,6 +119,16 @@ struct MultiTail {
 hipError_t launch_linear_multi(const DevMatrix* ms, int count, bool exact_w16, const uint16_t* x, int64_t M,
                                uint16_t* const* ys, const uint16_t* const* biases, hipStream_t stream);
 
+// Fused width search (eb_analyze.hip): per tile of kAnalyzeTileRows weight
+// rows, kAnalyzeSums partial sums (|ref|^2, then |full_b - ref|^2 for
+// b = 3..15, then |hw_b - ref|^2 for b = 3..8) over up to
+// kAnalyzeMaxSamples calibration rows.
+constexpr int kAnalyzeTileRows = 16;
+constexpr int kAnalyzeMaxSamples = 32;
+constexpr int kAnalyzeSums = 20;
+hipError_t launch_analyze_widths(const uint16_t* w, int N, int K, const uint16_t* x, int S, const float* max_abs,
+                                 float* partials, hipStream_t stream);
+
 // Prefill tile shape: 0 auto, 1 128 x 256, 2 256 x 256 (process-wide).
 void set_prefill_tiles(int mode);
 

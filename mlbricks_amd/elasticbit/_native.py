@@ -96,6 +96,7 @@ _sig("eb_forward_host", [_vp, _f32p, _f32p])
 _sig("eb_benchmark", [_vp, _f32p, _i, ctypes.POINTER(_d)])
 _sig("eb_forward", [_vp, _vp, _i64, _vp, _vp, _vp])
 _sig("eb_forward_multi", [_vp, _i, _vp, _i64, _vp, _vp, _vp])
+_sig("eb_analyze_widths_device", [_vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp])
 _sig("eb_materialize_fp16", [_vp, _vp, _vp])
 _sig("eb_unpack_codes", [_vp, _vp, _vp])
 _sig("eb_packed_linear", [_vp, _i, _i64, _vp, _vp, _i, _vp, _i, _i64, _i64, _i64, _vp, _vp])
@@ -239,6 +240,49 @@ def forward_torch_multi(matrices: Sequence["RuntimeMatrix"], input: torch.Tensor
     with torch.cuda.device(x.device):
         check(_lib.eb_forward_multi(handles, n, x.data_ptr(), rows_in, ys, bptr, stream_handle(x.device)))
     return outs
+
+
+ANALYZE_TILE_ROWS = 16
+ANALYZE_MAX_SAMPLES = 32
+ANALYZE_SUMS = 20
+ANALYZE_WIDTHS = tuple(range(3, 16))
+
+
+def width_errors_torch(weight: torch.Tensor, calibration16: torch.Tensor) -> tuple[np.ndarray, np.ndarray]:
+    """relL2 errors of every storage width b = 3..15 against ``F.linear(x, W)``
+    for fp16 CUDA weights ``[rows, cols]`` and fp16 calibration rows
+    ``[samples, cols]`` on the same device, from one fused pass over the
+    weights (eb_analyze_widths_device; the measurement of _selectBitsTorch,
+    core.py:112-195).  Returns ``(full, hw)``, float64 arrays indexed by
+    b - 3; ``hw`` equals ``full`` for b >= 9, where hardwareNative runs W16A16
+    (core.py:170-172)."""
+    if not weight.is_cuda or weight.dtype != torch.float16 or weight.dim() != 2:
+        raise ValueError("width search needs fp16 CUDA weights [rows, cols]")
+    if calibration16.device != weight.device or calibration16.dtype != torch.float16 or \
+            calibration16.dim() != 2 or calibration16.shape[1] != weight.shape[1]:
+        raise ValueError("calibration rows must be fp16 [samples, cols] on the weight device")
+    rows, cols = weight.shape
+    samples = calibration16.shape[0]
+    if samples == 0:
+        raise ValueError("calibrationData must contain at least one row")
+    w = weight.contiguous()
+    x = calibration16.contiguous()
+    tiles = -(-rows // ANALYZE_TILE_ROWS)
+    max_abs = w.abs().amax(dim=1).float().contiguous()
+    chunks = -(-samples // ANALYZE_MAX_SAMPLES)
+    partials = torch.empty((chunks, tiles, ANALYZE_SUMS), dtype=torch.float32, device=w.device)
+    with torch.cuda.device(w.device):
+        stream = stream_handle(w.device)
+        for c in range(chunks):
+            xs = x[c * ANALYZE_MAX_SAMPLES:(c + 1) * ANALYZE_MAX_SAMPLES]
+            check(_lib.eb_analyze_widths_device(w.data_ptr(), rows, cols, xs.data_ptr(), xs.shape[0],
+                                                max_abs.data_ptr(), partials[c].data_ptr(), stream))
+    sums = partials.double().sum(dim=(0, 1)).cpu().numpy()
+    den = max(float(np.sqrt(sums[0])), 1.0e-30)
+    full = np.sqrt(sums[1:14]) / den
+    hw = full.copy()
+    hw[:6] = np.sqrt(sums[14:20]) / den
+    return full, hw
 
 
 def set_prefill_tiles(mode: str) -> None:

@@ -101,12 +101,6 @@ def _moveBatch(batch: Any, device: torch.device) -> Any:
     return batch
 
 
-def _relativeL2Torch(reference: torch.Tensor, candidate: torch.Tensor) -> float:
-    ref = reference.float()
-    den = torch.linalg.vector_norm(ref).clamp_min(1.0e-30)
-    return float((torch.linalg.vector_norm(candidate.float() - ref) / den).item())
-
-
 @torch.inference_mode()
 def _selectBitsTorch(weight: torch.Tensor, calibration: np.ndarray, threshold: float
                      ) -> tuple[int, float, np.ndarray | None, np.ndarray | None]:
@@ -116,7 +110,10 @@ def _selectBitsTorch(weight: torch.Tensor, calibration: np.ndarray, threshold: f
     full = F.linear(x16, fp16(q*s)), and for b <= 8 also
     hw = fp16((x16.float() @ q^T) * s); the first b with
     max(relL2(ref, hw), relL2(ref, full)) <= threshold wins, ref = F.linear(x16, W16).
-    Returns the selected codes and scales so packing never re-quantizes.
+    The errors of all thirteen widths come from one fused HIP pass over the
+    weights (``width_errors_torch``); only the selected width is quantized
+    here, and its codes and scales are returned so packing never
+    re-quantizes.
     """
     if weight.device.type != "cuda":
         raise RuntimeError("ElasticBit GPU analyzer requires CUDA weights")
@@ -124,29 +121,29 @@ def _selectBitsTorch(weight: torch.Tensor, calibration: np.ndarray, threshold: f
         raise RuntimeError("ElasticBit GPU analyzer requires FP16 weights")
     if not np.isfinite(threshold) or float(threshold) < 0.0:
         raise ValueError("threshold must be a finite non-negative value")
+    native = _requireNative()
     x16 = torch.from_numpy(np.ascontiguousarray(calibration, dtype=np.float32)).to(
         device=weight.device, dtype=torch.float16)
-    reference = F.linear(x16, weight).detach()
-    w32 = weight.detach().float()
-    max_abs = w32.abs().amax(dim=1)
+    w = weight.detach()
+    full, hw = native.width_errors_torch(w, x16)
     for bits in range(3, 16):
-        qmax = float((1 << (bits - 1)) - 1)
-        scale = torch.where(max_abs > 0.0, max_abs / qmax, torch.ones_like(max_abs))
-        q = torch.round(w32 / scale[:, None]).clamp(min=-qmax, max=qmax)
-        deq16 = (q * scale[:, None]).to(torch.float16)
-        full_err = _relativeL2Torch(reference, F.linear(x16, deq16))
-        if bits <= 8:
-            idot = torch.matmul(x16.float(), q.transpose(0, 1))
-            hw_err = _relativeL2Torch(reference, (idot * scale[None, :]).to(torch.float16))
-        else:
-            hw_err = full_err
-        err = max(hw_err, full_err)
+        err = max(float(hw[bits - 3]), float(full[bits - 3]))
         if err <= float(threshold):
-            codes = np.ascontiguousarray(q.to(torch.int16).cpu().numpy(), dtype=np.int16)
-            scales = np.ascontiguousarray(scale.float().cpu().numpy(), dtype=np.float32)
-            return bits, float(err), codes, scales
-        del q, deq16
+            codes, scales = _quantizeRowsTorch(w, bits)
+            return bits, err, codes, scales
     return 16, 0.0, None, None
+
+
+def _quantizeRowsTorch(weight: torch.Tensor, bits: int) -> tuple[np.ndarray, np.ndarray]:
+    """Codes and row scales of one width, as core.py:142-155 forms them."""
+    w32 = weight.float()
+    max_abs = w32.abs().amax(dim=1)
+    qmax = float((1 << (bits - 1)) - 1)
+    scale = torch.where(max_abs > 0.0, max_abs / qmax, torch.ones_like(max_abs))
+    q = torch.round(w32 / scale[:, None]).clamp(min=-qmax, max=qmax)
+    codes = np.ascontiguousarray(q.to(torch.int16).cpu().numpy(), dtype=np.int16)
+    scales = np.ascontiguousarray(scale.float().cpu().numpy(), dtype=np.float32)
+    return codes, scales
 
 
 def _moduleDevice(module: nn.Module) -> torch.device:

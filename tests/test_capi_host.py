@@ -210,6 +210,17 @@ def test_device_calls_fail_loudly_without_device():
         m._materializeTorch()
 
 
+def test_analyze_widths_validates_arguments():
+    lib = native.lib()
+    p = ctypes.c_void_p(16)
+    assert lib.eb_analyze_widths_device(None, 16, 64, p, 4, p, p, None) != 0
+    assert "null pointer" in lib.eb_last_error().decode()
+    assert lib.eb_analyze_widths_device(p, 0, 64, p, 4, p, p, None) != 0
+    assert "rows and cols" in lib.eb_last_error().decode()
+    assert lib.eb_analyze_widths_device(p, 16, 64, p, 0, p, p, None) != 0
+    assert "samples must be in [1, 32]" in lib.eb_last_error().decode()
+
+
 def test_forward_multi_validates_before_any_device_work():
     lib = native.lib()
     m = RM._compressSelectedCodes(np.zeros((4, 32), np.int16), np.ones(4, np.float32), 10, 0.01, 0.0)
