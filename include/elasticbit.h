@@ -211,7 +211,7 @@ int eb_packed_linear(const void* x, int x_dtype, int64_t M, const uint8_t* packe
                      void* y, void* stream);
 
 /* Tuning control (no counterpart in the reference, which hands M > 1 to the
- * vendor GEMM): the output tile shape of the prefill route (M > 16, b <= 10,
+ * vendor GEMM): the output tile shape of the prefill route (M > 16, b <= 15,
  * hardwareNative or fullPrecision).  EB_PREFILL_TILES_AUTO (the default)
  * picks the shape with the fewer estimated rounds over the GPU's compute
  * units; NARROW forces 128 x 256 tiles; WIDE forces 256 x 256 tiles where M

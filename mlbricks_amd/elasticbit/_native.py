@@ -286,7 +286,7 @@ def width_errors_torch(weight: torch.Tensor, calibration16: torch.Tensor) -> tup
 
 
 def set_prefill_tiles(mode: str) -> None:
-    """Tile shape of the prefill route (M > 16, b <= 10): 'auto' (default,
+    """Tile shape of the prefill route (M > 16, b <= 15): 'auto' (default,
     picked by estimated rounds over the compute units), 'narrow' (128 x 256)
     or 'wide' (256 x 256).  Process-wide; a tuning and test control with no
     counterpart in the reference."""

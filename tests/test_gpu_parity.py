@@ -481,17 +481,19 @@ def wide_tiles(native):
     native.set_prefill_tiles("auto")
 
 
-@pytest.mark.parametrize("b", [3, 4, 5, 7, 8, 9, 10])
+@pytest.mark.parametrize("b", [3, 4, 5, 7, 8, 9, 10, 11, 12, 13, 15])
 @pytest.mark.parametrize("rows,cols,M", [(256, 128, 256), (300, 384, 700), (1000, 1000, 513), (520, 4096, 300)])
 @pytest.mark.parametrize("policy", ["hardwareNative", "fullPrecision"])
 def test_wide_prefill_tiles_match_oracle(native, wide_tiles, b, rows, cols, M, policy):
-    """M and rows of at least 256 with b <= 10: the 256 x 256 prefill tiles,
+    """M and rows of at least 256 with b <= 15: the 256 x 256 prefill tiles,
     ragged in M, N and K (1000 columns are not whole 128-column steps),
     against the fp64 oracle on a corner and torch fp32 on the whole output,
     with and without bias."""
     rng = np.random.default_rng(b * 1000 + rows + cols + M)
     q = _codes(rng, rows, cols, b)
-    s = rng.uniform(0.002, 0.05, size=rows).astype(np.float32)
+    # weights of the b = 10 magnitude at every width, so that no output
+    # leaves the fp16 range
+    s = (rng.uniform(0.002, 0.05, size=rows) * min(1.0, 511.0 / ((1 << (b - 1)) - 1))).astype(np.float32)
     m = native.RuntimeMatrix._compressSelectedCodes(q, s, b, 0.01, 0.0, decodePolicy=policy)
     x = _x16(rng, M, cols)
     y = m.forwardTorch(x)
@@ -508,7 +510,7 @@ def test_wide_prefill_tiles_match_oracle(native, wide_tiles, b, rows, cols, M, p
     assert torch.equal(m.forwardTorch(x, bias=bias), y + bias)
 
 
-@pytest.mark.parametrize("b", [4, 8, 10])
+@pytest.mark.parametrize("b", [4, 8, 10, 11, 12, 14, 15])
 @pytest.mark.parametrize("policy", ["hardwareNative", "fullPrecision"])
 def test_wide_prefill_one_hot_reproduces_decoded_weights(native, wide_tiles, b, policy):
     """One-hot activations through the 256 x 256 prefill tiles: every output
