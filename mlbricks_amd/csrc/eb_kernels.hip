@@ -502,6 +502,11 @@ struct GroupBits<B, kModeRaw> {
 #pragma unroll
         for (int t = 0; t < 4; ++t) w[t] = p[t];
     }
+    __device__ __forceinline__ void load32(const DevMatrix& m, uint32_t g) { load(m, g); }
+    __device__ __forceinline__ void copy_from(const GroupBits& o) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) w[t] = o.w[t];
+    }
     __device__ __forceinline__ half8 operand(int t, float) const { return __builtin_bit_cast(half8, w[t]); }
 };
 
@@ -1043,7 +1048,6 @@ template <int B, int MODE, int MI, int NB, int KS>
 __global__ __launch_bounds__(256 * KS) void linear_prefill_kernel(
     DevMatrix m, const uint16_t* __restrict__ x, int M, uint16_t* __restrict__ y,
     const uint16_t* __restrict__ bias, int mblocks, int nblocks, int tile0, int njobs, int per_xcd) {
-    static_assert(MODE != kModeRaw, "raw fp16 weights use linear_gemm_kernel");
     using Bits = GroupBits<B, MODE>;
     using Shape = PrefillShape<MI>;
     __shared__ __attribute__((aligned(16))) uint8_t xs[Shape::kLds];
@@ -1205,8 +1209,8 @@ __global__ __launch_bounds__(256 * KS) void linear_prefill_kernel(
     // most 10 bits the register budget holds a third B buffer, so B is
     // prefetched two steps ahead; the buffers rotate by unrolling, so no
     // register copy is needed.
-    constexpr int kBDist = (KS == 2 && B <= 10) ? 2 : 1;
-    constexpr int kBLoads = NB * kPL * group_loads<B>();   // B loads per step per wave
+    constexpr int kBDist = (KS == 2 && MODE != kModeRaw && B <= 10) ? 2 : 1;
+    constexpr int kBLoads = NB * kPL * GroupLoads<B, MODE>::value;   // B loads per step per wave
     auto step = [&](const Bits (&cur)[NB][kPL], Bits (&next)[NB][kPL], int st) {
         load_b(next, st + kBDist);
         __builtin_amdgcn_sched_barrier(0);
@@ -1392,9 +1396,9 @@ template <int B, int MODE>
 __global__ __launch_bounds__(256) void linear_prefill_wide_kernel(
     DevMatrix m, const uint16_t* __restrict__ x, int M, uint16_t* __restrict__ y,
     const uint16_t* __restrict__ bias, int mblocks, int nblocks, int njobs, int per_xcd) {
-    static_assert(MODE != kModeRaw && B <= EBK_WIDE_MAX_BITS, "wide tiles take packed widths only");
+    static_assert(B <= EBK_WIDE_MAX_BITS, "width beyond the wide kernel's ring");
     using Bits = GroupBits<B, MODE>;
-    constexpr int GL = group_loads<B>();           // vector loads per group
+    constexpr int GL = GroupLoads<B, MODE>::value;  // vector loads per group
     __shared__ __attribute__((aligned(16))) uint8_t xs[4 * kWHalf];
 
     const int xcd = blockIdx.x & 7;
@@ -1803,6 +1807,11 @@ constexpr int kDecodeMaxM = 16;
 #ifndef EBK_PREFILL_WIDE
 #define EBK_PREFILL_WIDE 1
 #endif
+// Raw fp16 weights (b = 16) through the prefill kernels (their B operand
+// is the stored fp16, no decode); linear_gemm_kernel otherwise.
+#ifndef EBK_PREFILL_RAW
+#define EBK_PREFILL_RAW 1
+#endif
 #ifndef EBK_GEMV_MODES
 #define EBK_GEMV_MODES ((1 << kModeQ) | (1 << kModeRaw))
 #endif
@@ -1849,10 +1858,11 @@ hipError_t run_linear_mode(const DevMatrix& m, const uint16_t* x, int64_t M, uin
         }
     } else if (mt.count > 1) {
         return hipErrorInvalidValue;      // the launcher splits prefill per matrix
-    } else if (MODE != kModeRaw && B <= EBK_WIDE_MAX_BITS && EBK_PREFILL_WIDE && xvec && M >= kWRows && m.rows >= kWN &&
+    } else if (B <= EBK_WIDE_MAX_BITS && (MODE != kModeRaw || EBK_PREFILL_RAW) && EBK_PREFILL_WIDE && xvec &&
+               M >= kWRows && m.rows >= kWN &&
                static_cast<uint64_t>(M) * m.cols * 2 < (uint64_t(1) << 32) &&
                prefer_wide_tiles(M, m.rows, device_cu_count())) {
-        if constexpr (MODE != kModeRaw && B <= EBK_WIDE_MAX_BITS) {
+        if constexpr (B <= EBK_WIDE_MAX_BITS && (MODE != kModeRaw || EBK_PREFILL_RAW)) {
             const int mblocks = static_cast<int>((M + kWRows - 1) / kWRows);
             const int nblocks = (m.rows + kWN - 1) / kWN;
             const int jobs = mblocks * nblocks;
@@ -1860,8 +1870,9 @@ hipError_t run_linear_mode(const DevMatrix& m, const uint16_t* x, int64_t M, uin
             hipLaunchKernelGGL((linear_prefill_wide_kernel<B, MODE>), dim3(8 * per_xcd), dim3(256), 0, s, m, x,
                                static_cast<int>(M), y, bias, mblocks, nblocks, jobs, per_xcd);
         }
-    } else if (MODE != kModeRaw && xvec && static_cast<uint64_t>(M) * m.cols * 2 < (uint64_t(1) << 32)) {
-        if constexpr (MODE != kModeRaw) {
+    } else if ((MODE != kModeRaw || EBK_PREFILL_RAW) && xvec &&
+               static_cast<uint64_t>(M) * m.cols * 2 < (uint64_t(1) << 32)) {
+        if constexpr (MODE != kModeRaw || EBK_PREFILL_RAW) {
             // Full tiles are 128 x 256.  When the last round of full tiles
             // would leave at least half the CUs idle, its tiles run as two
             // 128 x 128 halves instead, so it takes half a round.
