@@ -1390,7 +1390,10 @@ constexpr int kWRows = 256;                 // activation rows per workgroup
 constexpr int kWN = 256;                    // weight rows per workgroup (4 waves x 64)
 constexpr int kWHalfRow = kPRow / 2;        // bytes per staged row of a half step (64 columns)
 constexpr int kWHalf = kWRows * kWHalfRow;  // bytes per half-stage (32 KB)
-constexpr int kWGroupM = 4;                 // activation blocks per tile-order group
+#ifndef EBK_WIDE_GROUP_M
+#define EBK_WIDE_GROUP_M 4
+#endif
+constexpr int kWGroupM = EBK_WIDE_GROUP_M;  // activation blocks per tile-order group
 
 template <int B, int MODE>
 __global__ __launch_bounds__(256) void linear_prefill_wide_kernel(

@@ -209,6 +209,27 @@ def test_forward_ragged_shapes(native, b, rows, cols, M):
     assert _rel_max(y, ref) <= TOL
 
 
+@pytest.mark.parametrize("rows,cols,M", [(7, 13, 40), (33, 65, 40), (5, 1000, 40), (300, 1000, 513),
+                                         (520, 1000, 300), (100, 2056, 64)])
+@pytest.mark.parametrize("tiles", ["auto", "wide"])
+def test_fp16_fallback_prefill_ragged(native, rows, cols, M, tiles):
+    """b = 16 (raw fp16 weights) through the prefill kernels: K not a whole
+    number of 32-column groups (the padded tail of the last group must
+    contribute nothing), ragged M and N, both tile shapes; against the fp64
+    oracle of the W16A16 product."""
+    rng = np.random.default_rng(rows * 7 + cols + M)
+    w = (rng.standard_normal((rows, cols)) * 0.05).astype(np.float32)
+    native.set_prefill_tiles(tiles)
+    try:
+        m = native.RuntimeMatrix._compressSelected(w, 16, 0.01, 0.0)
+        x = _x16(rng, M, cols)
+        y = m.forwardTorch(x).float().cpu().numpy()
+    finally:
+        native.set_prefill_tiles("auto")
+    ref = _reference(ora.pack_weights(w, 16), None, rows, cols, 16, x.cpu().numpy().view(np.uint16))
+    assert _rel_max(y, ref) <= TOL
+
+
 @pytest.mark.parametrize("M", [2, 4, 8, 16])
 @pytest.mark.parametrize("cols,aligned", [(4096, True), (4608, True), (11008, True), (1000, True), (4096, False)])
 @pytest.mark.parametrize("b", [8, 10, 13])
@@ -296,6 +317,19 @@ def test_forward_multi_matches_single_forwards(native, group, M, cols, aligned):
                          x.cpu().numpy().view(np.uint16), policy)
         y0 = native.forward_torch_multi(mats, x)[0]
         assert _rel_max(y0.float().cpu().numpy(), ref) <= TOL
+
+
+def test_forward_multi_through_the_public_runtime_matrix(native):
+    """RuntimeMatrix.forwardTorchMulti (the Python surface a model calls)
+    returns each matrix's own forward."""
+    from mlbricks_amd.elasticbit import RuntimeMatrix
+    rng = np.random.default_rng(21)
+    mats = [RuntimeMatrix._compressSelectedCodes(_codes(rng, r, 512, 9), rng.uniform(0.002, 0.05, r).astype(np.float32),
+                                                 9, 0.01, 0.0) for r in (512, 128, 128)]
+    x = _x16(rng, 1, 512)
+    ys = RuntimeMatrix.forwardTorchMulti(mats, x)
+    for m, y in zip(mats, ys):
+        assert torch.equal(y, m.forward(x))
 
 
 def test_forward_multi_rejects_mismatched_inputs(native):
