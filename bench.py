@@ -14,6 +14,10 @@ bytes counted at the storage width: ceil(N*K*b/8) + 4N + 2MK + 2MN.
 Also reported (not the headline): the prefill GEMM of configs[3] (4096->14336,
 M=2048) in TFLOP/s, and the oracle's OpenMP CPU GEMV on the host's cores.
 
+Every configuration beside the reference's execution format (markdown table):
+
+    python bench.py --all-configs
+
 Profiling helpers (same file, so the committed summaries name committed code):
 
     python bench.py --traffic-probe      # eager launches for rocprofv3 --pmc passes
@@ -65,6 +69,9 @@ def parse_args() -> argparse.Namespace:
                    help="run eager GEMV/prefill launches and a calibration copy for rocprofv3 --pmc")
     p.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
     p.add_argument("--summarize-trace", metavar="KERNEL_STATS_CSV")
+    p.add_argument("--all-configs", action="store_true",
+                   help="time every BASELINE configuration (0-3) beside the reference's execution format; "
+                        "prints a markdown table")
     return p.parse_args()
 
 
@@ -272,6 +279,94 @@ def reference_route(args) -> dict:
     return out
 
 
+def all_configs(args) -> int:
+    """Every BASELINE configuration that runs on one GPU, compressed by the
+    real ElasticBit.compress, timed like the headline (HIP graph, events on
+    the launch stream, weight copies rotated past the MALL for M <= 16),
+    beside the reference's execution format on the same weights: W16A16
+    decode for M = 1 at b = 9..15 (this build's GEMV over fp16 storage), and
+    materialize + F.linear (core.py:462-471) for M > 1."""
+    import torch
+
+    from mlbricks_amd.elasticbit import _native as native
+
+    def weight0(rows, cols):
+        # configs[0]: N(0, 0.02) from seed 0, no outlier columns
+        return (torch.randn(rows, cols, generator=torch.Generator().manual_seed(0)) * 0.02).half()
+
+    def compress(rows, cols, thr, calib_rows, outliers=True):
+        from mlbricks_amd import ElasticBit
+
+        lin = torch.nn.Linear(cols, rows, bias=False)
+        with torch.no_grad():
+            lin.weight.copy_((make_weight(rows, cols) if outliers else weight0(rows, cols)).float())
+        model = torch.nn.Sequential(lin).cuda().half().eval()
+        calib = torch.randn(calib_rows, cols, generator=torch.Generator().manual_seed(2)).half()
+        ElasticBit.compress(model, calib, thr)
+        return model[0]
+
+    def ours(mats, M, steps):
+        cols, rows = mats[0].cols, mats[0].rows
+        x = torch.randn(M, cols, generator=torch.Generator().manual_seed(1)).half().cuda()
+        ys = [torch.empty(M, rows, dtype=torch.float16, device="cuda") for _ in mats]
+        ms = time_graph([lambda m=m, y=y: m.forwardTorch(x, out=y) for m, y in zip(mats, ys)], steps, steps // 10)
+        return ms / steps * 1e3
+
+    def reference(mats, M, steps):
+        nm = mats[0]
+        cols, rows = nm.cols, nm.rows
+        x = torch.randn(M, cols, generator=torch.Generator().manual_seed(1)).half().cuda()
+        if M == 1 and nm.storageBits >= 9:
+            w16 = [native.RuntimeMatrix._compressSelected(m._materializeTorch().float().cpu().numpy(), 16, 0.01, 0.0)
+                   for m in mats[: max(2, -(-2 * MALL_BYTES // (2 * rows * cols)) + 1)]]
+            ys = [torch.empty(1, rows, dtype=torch.float16, device="cuda") for _ in w16]
+            ms = time_graph([lambda m=m, y=y: m.forwardTorch(x, out=y) for m, y in zip(w16, ys)], steps, steps // 10)
+            return ms / steps * 1e3, "W16A16 GEMV"
+        if M == 1:
+            return None, "W4/W8 GEMV (not timed)"
+        wbuf = torch.empty(rows, cols, dtype=torch.float16, device="cuda")
+        y = torch.empty(M, rows, dtype=torch.float16, device="cuda")
+
+        def mk(m):
+            def run():
+                native.check(native.lib().eb_materialize_fp16(m._h, wbuf.data_ptr(), native.stream_handle(wbuf.device)))
+                torch.matmul(x, wbuf.t(), out=y)
+            return run
+        ms = time_graph([mk(m) for m in mats], steps, steps // 10)
+        return ms / steps * 1e3, "materialize + F.linear"
+
+    lines = ["| config | N x K | thr | b | M | ours us | GB/s (% HBM) | TFLOP/s (% fp16) | reference route | ref us |",
+             "|---|---|---|---|---|---|---|---|---|---|"]
+
+    def row(cfg, layer, thr, Ms, rotate):
+        nm = layer.matrix._native
+        rows, cols, bits = nm.rows, nm.cols, nm.storageBits
+        n_copies = max(2, -(-2 * MALL_BYTES // nm.executionBytes) + 1) if rotate else 1
+        mats = copies_of(layer, n_copies) if n_copies > 1 else [nm]
+        for M in Ms:
+            steps = 1000 if M <= 16 else 50
+            us = ours(mats, M, steps)
+            nbytes = algorithmic_bytes(rows, cols, bits, M)
+            gbs = nbytes / (us * 1e-6) / 1e9
+            tf = 2.0 * M * rows * cols / (us * 1e-6) / 1e12
+            ref_us, ref_what = reference(mats, M, 200 if M <= 16 else 20)
+            ref_txt = f"{ref_us:.2f}" if ref_us is not None else "-"
+            lines.append(f"| {cfg} | {rows} x {cols} | {thr} | {bits} | {M} | {us:.2f} | {gbs:.0f} "
+                         f"({100 * gbs / HBM_PEAK_GBS:.1f}%) | {tf:.1f} ({100 * tf / FP16_PEAK_TFLOPS:.1f}%) | "
+                         f"{ref_what} | {ref_txt} |")
+            log(lines[-1])
+        del mats
+
+    row("configs[0]", compress(1536, 384, 0.01, 256, outliers=False), 0.01, (256,), rotate=False)
+    row("configs[1]", compress(4096, 4096, 0.01, 512), 0.01, (1,), rotate=True)
+    for thr in (0.005, 0.01, 0.02):
+        for rows, cols in ((11008, 4096), (4096, 11008)):
+            row("configs[2]", compress(rows, cols, thr, 512), thr, (1, 4, 16), rotate=True)
+    row("configs[3]", compress(14336, 4096, 0.01, 512), 0.01, (2048,), rotate=False)
+    print("\n".join(lines), flush=True)
+    return 0
+
+
 def cpu_baseline(layer, seconds: float) -> dict:
     """The oracle's OpenMP GEMV (fp32 accumulate) over the same matrix and the
     same algorithmic bytes, on this host's cores (bounded to ~`seconds`)."""
@@ -464,6 +559,8 @@ def main() -> int:
 
     if args.traffic_probe:
         return traffic_probe(args)
+    if args.all_configs:
+        return all_configs(args)
 
     g = bench_gemv(args)
     ceiling = read_ceiling(g["bytes"], g["copies"], args.steps, args.warmup)
