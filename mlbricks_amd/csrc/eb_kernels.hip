@@ -1819,6 +1819,22 @@ constexpr int kDecodeMaxM = 16;
 #define EBK_GEMV_MODES ((1 << kModeQ) | (1 << kModeRaw))
 #endif
 
+// Whether linear_gemv_kernel takes an M = 1 launch (else
+// linear_decode_kernel).  Measured on MI355X at M = 1 over rotated copies:
+// with K at most 16 tiles (2048 columns) half or more of the 16 waves idle
+// and the decode kernel is faster (4096 x 1024: 3.4-3.9 us against
+// 3.7-5.3 us; 4096 x 2048 from b = 10); at b = 11 (three planes, four loads
+// per group) the decode kernel is 2-3% faster at every N; at b <= 4 with
+// more than 256 row tiles 4-11% faster (14336 x 4096 b = 4: 8.0 against
+// 9.0 us).  Elsewhere the GEMV kernel is ahead by up to 24% (1024 x 4096).
+template <int B, int MODE>
+inline bool gemv_takes(const DevMatrix& m) {
+    if (!((EBK_GEMV_MODES >> MODE) & 1)) return false;
+    if (m.spr <= kGemvMaxSteps / 2 || m.spr > kGemvMaxSteps) return false;
+    if (MODE != kModeRaw && (B == 11 || (B <= 4 && m.rtiles > 256))) return false;
+    return true;
+}
+
 // Whether the 256 x 256 prefill tiles finish before the 128 x 256 ones.
 // Cost in rounds of 128 x 256 tiles over the CUs: a 256 x 256 tile takes
 // about 1.7 of them (measured on MI355X, 14336 x 4096 b = 10: 116 us per
@@ -1844,7 +1860,7 @@ template <int B, int MODE>
 hipError_t run_linear_mode(const DevMatrix& m, const uint16_t* x, int64_t M, uint16_t* y,
                            const uint16_t* bias, int xvec, hipStream_t s, const MultiTail& mt) {
     const int tiles = mt.count > 1 ? mt.tile0[mt.count - 2] + mt.m[mt.count - 2].rtiles : m.rtiles;
-    if (M == 1 && xvec == 2 && m.spr <= kGemvMaxSteps && ((EBK_GEMV_MODES >> MODE) & 1)) {
+    if (M == 1 && xvec == 2 && gemv_takes<B, MODE>(m)) {
         hipLaunchKernelGGL((linear_gemv_kernel<B, MODE>), dim3(tiles), dim3(64 * kGemvWaves),
                            static_cast<size_t>(m.cols) * 2, s, m, x, y, bias, mt);
     } else if (M <= kDecodeMaxM) {

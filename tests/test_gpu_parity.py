@@ -146,12 +146,14 @@ def test_one_hot_activations_reproduce_decoded_weights(native, b, M, policy):
 
 
 @pytest.mark.parametrize("b", list(range(3, 16)) + [16])
-@pytest.mark.parametrize("rows,cols", [(1, 128), (17, 384), (100, 2048), (33, 4096), (16, 4224)])
+@pytest.mark.parametrize("rows,cols", [(1, 128), (17, 384), (100, 2048), (40, 2176), (24, 3072), (33, 4096),
+                                       (16, 4224)])
 @pytest.mark.parametrize("policy", ["hardwareNative", "fullPrecision"])
 def test_gemv_whole_tile_rows(native, b, rows, cols, policy):
     """M = 1 with 16-byte aligned x and whole 128-column tiles: the 16-wave
-    GEMV kernel up to 4096 columns (4224 takes the pipelined decode kernel),
-    against the oracle, with and without bias."""
+    GEMV kernel for 2176 to 4096 columns (17 to 32 tiles, b != 11), the
+    pipelined decode kernel for the others, against the oracle, with and
+    without bias."""
     rng = np.random.default_rng(b * 7 + rows + cols)
     if b == 16:
         w = (rng.standard_normal((rows, cols)) * 0.05).astype(np.float32)
@@ -174,10 +176,12 @@ def test_gemv_whole_tile_rows(native, b, rows, cols, policy):
 
 @pytest.mark.parametrize("b", [3, 4, 9, 10, 11, 15, 16])
 @pytest.mark.parametrize("policy", ["hardwareNative", "fullPrecision"])
-def test_gemv_one_hot_reproduces_decoded_weights(native, b, policy):
-    """M = 1 one-hot activations through the GEMV kernel: y[n] is the decoded
-    weight w[n][k] (or fp16(s*q) in integer-dot mode, the same bits)."""
-    rows, cols = 40, 512
+@pytest.mark.parametrize("cols", [512, 2304])
+def test_gemv_one_hot_reproduces_decoded_weights(native, b, policy, cols):
+    """M = 1 one-hot activations through the GEMV kernel (2304 columns) and
+    the decode kernel (512): y[n] is the decoded weight w[n][k] (or fp16(s*q)
+    in integer-dot mode, the same bits)."""
+    rows = 40
     rng = np.random.default_rng(b)
     if b == 16:
         w = (rng.standard_normal((rows, cols)) * 0.05).astype(np.float32)
