@@ -50,8 +50,8 @@ __host__ __device__ inline size_t group_slot(int row, int grp, int spr) {
 struct DevMatrix {
     const uint8_t* p8 = nullptr;    // [G][32] bytes
     const uint8_t* p4 = nullptr;    // [G][16]
-    const uint8_t* p2 = nullptr;    // [G][8]
-    const uint8_t* p1 = nullptr;    // [G][4]
+    const uint8_t* p2 = nullptr;    // [G][8], or [G][12] with the 1-bit word (merged tail)
+    const uint8_t* p1 = nullptr;    // [G][4], unused with a merged tail
     const uint16_t* w16 = nullptr;  // [G][32] fp16, b = 16 only
     const float* scales = nullptr;  // [rows], b <= 15
     int rows = 0;
@@ -76,11 +76,24 @@ struct DevMatrixOut {
     int bits = 0;
 };
 
+// Widths with a wide plane and both a 2-bit and a 1-bit plane (b = 7, 11,
+// 15) keep the two small ones together: per group 12 bytes in the width-2
+// array (the two 2-bit words, then the 1-bit word), so a lane reads them
+// with one load instead of two.  Measured on MI355X at M = 1 and 4:
+// 11008 x 4096 b = 11 13.66 -> 13.23 us, b = 15 0.4-2% faster; b = 3 (whose
+// only planes these are) was no faster and keeps them apart.
+#ifndef EBK_MERGED_TAIL
+#define EBK_MERGED_TAIL 1
+#endif
+constexpr bool merged_tail(int bits) { return EBK_MERGED_TAIL && bits >= 7 && bits != 16 && (bits & 3) == 3; }
+
 // Bytes of the plane of width `width` (8, 4, 2, 1; 16 = raw fp16) for
-// `groups` slots (rtiles * spr * 64); 0 when b has no such plane.
+// `groups` slots (rtiles * spr * 64); 0 when b has no such plane (or keeps
+// it in the merged tail).
 inline size_t plane_bytes(int bits, int width, size_t groups) {
     if (bits == 16) return width == 16 ? groups * 64u : 0u;
     if (width == 16 || (bits & width) == 0) return 0u;
+    if (merged_tail(bits)) return width == 1 ? 0u : width == 2 ? groups * 12u : groups * 4u * width;
     return groups * 4u * static_cast<size_t>(width);
 }
 

@@ -37,6 +37,7 @@ struct Planes {
     static constexpr bool h4 = (B & 4) != 0;
     static constexpr bool h2 = (B & 2) != 0;
     static constexpr bool h1 = (B & 1) != 0;
+    static constexpr bool h21 = merged_tail(B);        // 2- and 1-bit words in one 12-byte slot
     static constexpr int off4 = h8 ? 8 : 0;           // bit offset of each plane in u
     static constexpr int off2 = off4 + (h4 ? 4 : 0);
     static constexpr int off1 = off2 + (h2 ? 2 : 0);
@@ -76,12 +77,17 @@ __device__ __forceinline__ void raw_load(const DevMatrix& m, size_t g, Raw<B>& r
         const uint4 a = reinterpret_cast<const uint4*>(m.p4)[g];
         r.d4[0] = a.x; r.d4[1] = a.y; r.d4[2] = a.z; r.d4[3] = a.w;
     }
-    if constexpr (P::h2) {
-        const uint2 a = reinterpret_cast<const uint2*>(m.p2)[g];
-        r.d2[0] = a.x; r.d2[1] = a.y;
-    }
-    if constexpr (P::h1) {
-        r.d1 = reinterpret_cast<const uint32_t*>(m.p1)[g];
+    if constexpr (P::h21) {
+        const uint3 a = *reinterpret_cast<const uint3*>(m.p2 + g * 12);
+        r.d2[0] = a.x; r.d2[1] = a.y; r.d1 = a.z;
+    } else {
+        if constexpr (P::h2) {
+            const uint2 a = reinterpret_cast<const uint2*>(m.p2)[g];
+            r.d2[0] = a.x; r.d2[1] = a.y;
+        }
+        if constexpr (P::h1) {
+            r.d1 = reinterpret_cast<const uint32_t*>(m.p1)[g];
+        }
     }
 }
 
@@ -102,12 +108,17 @@ __device__ __forceinline__ void raw_load32(const DevMatrix& m, uint32_t g, Raw<B
         const uint4 a = *reinterpret_cast<const uint4*>(m.p4 + g * 16u);
         r.d4[0] = a.x; r.d4[1] = a.y; r.d4[2] = a.z; r.d4[3] = a.w;
     }
-    if constexpr (P::h2) {
-        const uint2 a = *reinterpret_cast<const uint2*>(m.p2 + g * 8u);
-        r.d2[0] = a.x; r.d2[1] = a.y;
-    }
-    if constexpr (P::h1) {
-        r.d1 = *reinterpret_cast<const uint32_t*>(m.p1 + g * 4u);
+    if constexpr (P::h21) {
+        const uint3 a = *reinterpret_cast<const uint3*>(m.p2 + g * 12u);
+        r.d2[0] = a.x; r.d2[1] = a.y; r.d1 = a.z;
+    } else {
+        if constexpr (P::h2) {
+            const uint2 a = *reinterpret_cast<const uint2*>(m.p2 + g * 8u);
+            r.d2[0] = a.x; r.d2[1] = a.y;
+        }
+        if constexpr (P::h1) {
+            r.d1 = *reinterpret_cast<const uint32_t*>(m.p1 + g * 4u);
+        }
     }
 }
 
@@ -274,8 +285,12 @@ __global__ void repack_kernel(const uint8_t* __restrict__ canon, uint64_t canon_
         p[1] = make_uint4(d8[4], d8[5], d8[6], d8[7]);
     }
     if constexpr (P::h4) reinterpret_cast<uint4*>(out.p4)[g] = make_uint4(d4[0], d4[1], d4[2], d4[3]);
-    if constexpr (P::h2) reinterpret_cast<uint2*>(out.p2)[g] = make_uint2(d2[0], d2[1]);
-    if constexpr (P::h1) reinterpret_cast<uint32_t*>(out.p1)[g] = d1;
+    if constexpr (P::h21) {
+        *reinterpret_cast<uint3*>(out.p2 + g * 12) = make_uint3(d2[0], d2[1], d1);
+    } else {
+        if constexpr (P::h2) reinterpret_cast<uint2*>(out.p2)[g] = make_uint2(d2[0], d2[1]);
+        if constexpr (P::h1) reinterpret_cast<uint32_t*>(out.p1)[g] = d1;
+    }
 }
 
 __global__ void repack16_kernel(const uint16_t* __restrict__ canon, DevMatrixOut out, uint64_t slots) {
@@ -515,8 +530,8 @@ template <int B, int MODE>
 struct GroupLoads {
     static constexpr int value =
         MODE == kModeRaw ? 4
-                         : (Planes<B>::h8 ? 2 : 0) + (Planes<B>::h4 ? 1 : 0) + (Planes<B>::h2 ? 1 : 0) +
-                               (Planes<B>::h1 ? 1 : 0);
+                         : (Planes<B>::h8 ? 2 : 0) + (Planes<B>::h4 ? 1 : 0) +
+                               (Planes<B>::h21 ? 1 : (Planes<B>::h2 ? 1 : 0) + (Planes<B>::h1 ? 1 : 0));
 };
 
 // Eight activations x[r][k .. k+8) as one uint4, zero at and beyond `cols`.
@@ -1027,7 +1042,8 @@ constexpr int kPGroupM = 4;                // activation blocks per tile-order g
 // Vector-memory instructions one GroupBits::load32 issues (kModeQ / kModeW).
 template <int B>
 constexpr int group_loads() {
-    return (Planes<B>::h8 ? 2 : 0) + (Planes<B>::h4 ? 1 : 0) + (Planes<B>::h2 ? 1 : 0) + (Planes<B>::h1 ? 1 : 0);
+    return (Planes<B>::h8 ? 2 : 0) + (Planes<B>::h4 ? 1 : 0) +
+           (Planes<B>::h21 ? 1 : (Planes<B>::h2 ? 1 : 0) + (Planes<B>::h1 ? 1 : 0));
 }
 
 // Prefill tile geometry for MI 32-row activation blocks per wave.
