@@ -1839,15 +1839,17 @@ constexpr int kDecodeMaxM = 16;
 // linear_decode_kernel).  Measured on MI355X at M = 1 over rotated copies:
 // with K at most 16 tiles (2048 columns) half or more of the 16 waves idle
 // and the decode kernel is faster (4096 x 1024: 3.4-3.9 us against
-// 3.7-5.3 us; 4096 x 2048 from b = 10); at b = 11 (three planes, four loads
-// per group) the decode kernel is 2-3% faster at every N; at b <= 4 with
-// more than 256 row tiles 4-11% faster (14336 x 4096 b = 4: 8.0 against
-// 9.0 us).  Elsewhere the GEMV kernel is ahead by up to 24% (1024 x 4096).
+// 3.7-5.3 us; 4096 x 2048 from b = 10); at b = 11 the two are even or the
+// decode kernel ahead (4096 x 3072: 5.59 against 6.24 us); at b <= 7 with
+// more than 256 row tiles (at most 28 bytes per lane and group) the decode
+// kernel is 4-11% faster (14336 x 4096 b = 4: 8.0 against 9.0 us, b = 7:
+// 11.7 against 12.5 us).  Elsewhere the GEMV kernel is ahead by up to 24%
+// (1024 x 4096).
 template <int B, int MODE>
 inline bool gemv_takes(const DevMatrix& m) {
     if (!((EBK_GEMV_MODES >> MODE) & 1)) return false;
     if (m.spr <= kGemvMaxSteps / 2 || m.spr > kGemvMaxSteps) return false;
-    if (MODE != kModeRaw && (B == 11 || (B <= 4 && m.rtiles > 256))) return false;
+    if (MODE != kModeRaw && (B == 11 || (B <= 7 && m.rtiles > 256))) return false;
     return true;
 }
 
