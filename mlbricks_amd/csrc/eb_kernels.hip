@@ -1878,6 +1878,13 @@ template <int B, int MODE>
 hipError_t run_linear_mode(const DevMatrix& m, const uint16_t* x, int64_t M, uint16_t* y,
                            const uint16_t* bias, int xvec, hipStream_t s, const MultiTail& mt) {
     const int tiles = mt.count > 1 ? mt.tile0[mt.count - 2] + mt.m[mt.count - 2].rtiles : m.rtiles;
+    // The prefill kernels address x and the weight planes with 32-bit byte
+    // offsets: x below 4 GiB, and the widest plane (32 bytes per group; the
+    // raw fp16 weights load through 64-bit addresses) below 4 GiB.  Larger
+    // operands take linear_gemm_kernel, whose addressing is 64-bit.
+    const uint64_t groups = static_cast<uint64_t>(m.rtiles) * m.spr * kTileSlots;
+    const bool offsets32 = static_cast<uint64_t>(M) * m.cols * 2 < (uint64_t(1) << 32) &&
+                           (MODE == kModeRaw || groups * 32u < (uint64_t(1) << 32));
     if (M == 1 && xvec == 2 && gemv_takes<B, MODE>(m)) {
         hipLaunchKernelGGL((linear_gemv_kernel<B, MODE>), dim3(tiles), dim3(64 * kGemvWaves),
                            static_cast<size_t>(m.cols) * 2, s, m, x, y, bias, mt);
@@ -1896,8 +1903,7 @@ hipError_t run_linear_mode(const DevMatrix& m, const uint16_t* x, int64_t M, uin
     } else if (mt.count > 1) {
         return hipErrorInvalidValue;      // the launcher splits prefill per matrix
     } else if (B <= EBK_WIDE_MAX_BITS && (MODE != kModeRaw || EBK_PREFILL_RAW) && EBK_PREFILL_WIDE && xvec &&
-               M >= kWRows && m.rows >= kWN &&
-               static_cast<uint64_t>(M) * m.cols * 2 < (uint64_t(1) << 32) &&
+               offsets32 && M >= kWRows && m.rows >= kWN &&
                prefer_wide_tiles(M, m.rows, device_cu_count())) {
         if constexpr (B <= EBK_WIDE_MAX_BITS && (MODE != kModeRaw || EBK_PREFILL_RAW)) {
             const int mblocks = static_cast<int>((M + kWRows - 1) / kWRows);
@@ -1907,8 +1913,7 @@ hipError_t run_linear_mode(const DevMatrix& m, const uint16_t* x, int64_t M, uin
             hipLaunchKernelGGL((linear_prefill_wide_kernel<B, MODE>), dim3(8 * per_xcd), dim3(256), 0, s, m, x,
                                static_cast<int>(M), y, bias, mblocks, nblocks, jobs, per_xcd);
         }
-    } else if ((MODE != kModeRaw || EBK_PREFILL_RAW) && xvec &&
-               static_cast<uint64_t>(M) * m.cols * 2 < (uint64_t(1) << 32)) {
+    } else if ((MODE != kModeRaw || EBK_PREFILL_RAW) && xvec && offsets32) {
         if constexpr (MODE != kModeRaw || EBK_PREFILL_RAW) {
             // Full tiles are 128 x 256.  When the last round of full tiles
             // would leave at least half the CUs idle, its tiles run as two
