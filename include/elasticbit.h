@@ -171,9 +171,10 @@ int eb_forward(const eb_matrix* m, const void* x_f16, int64_t M, void* y_f16,
  * weights of Q/K/V and Gate/Up and runs one F.linear, stage2f.py:382-420):
  *   ys[j][M][rows_j] = x[M][cols] . W_j^T (+ biases[j]),  j < count,
  * each as eb_forward computes it.  Every matrix has the same cols and lives
- * on one device; biases may be NULL, as may any biases[j].  For M <= 16,
- * consecutive matrices of one width and policy (up to four) share one
- * launch, so the decode of a QKV or Gate/Up group pays one launch. */
+ * on one device; biases may be NULL, as may any biases[j].  Consecutive
+ * matrices of one width and policy (up to four) share one launch for
+ * M <= 16, and up to M = 64 where the decode kernel is the faster route for
+ * each of them, so the decode of a QKV or Gate/Up group pays one launch. */
 int eb_forward_multi(const eb_matrix* const* ms, int count, const void* x_f16, int64_t M,
                      void* const* ys_f16, const void* const* biases_f16, void* stream);
 

@@ -559,34 +559,41 @@ __device__ __forceinline__ void decode_load_batch(const DevMatrix& m, Bits (&bit
 
 // Activation operands of one workgroup batch (steps base + wave*GPL + j):
 // from the LDS copy, or from global memory, zero past the last step.
-template <int GPL, int XL>
-__device__ __forceinline__ void decode_activations(half8 (&a)[GPL][4], const DevMatrix& m, int base, int wave,
-                                                   int quarter, bool m_ok, int steps,
-                                                   const uint16_t* __restrict__ xrow, const uint16_t* xsrow,
-                                                   int xvec) {
+// Block mb holds activation rows 16 mb .. 16 mb + 15.
+template <int GPL, int XL, int MB>
+__device__ __forceinline__ void decode_activations(half8 (&a)[MB][GPL][4], const DevMatrix& m, int base, int wave,
+                                                   int quarter, const bool (&m_ok)[MB], int steps,
+                                                   const uint16_t* const (&xrow)[MB],
+                                                   const uint16_t* const (&xsrow)[MB], int xvec) {
     const int first = base + wave * GPL;
 #pragma unroll
-    for (int j = 0; j < GPL; ++j) {
-        const int k0 = ((first + j) * kTileGroups + quarter) * kGroup;
-        const bool ok = m_ok && first + j < steps;
-        if constexpr (XL != 0) {
+    for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                a[j][t] = ok ? *reinterpret_cast<const half8*>(xsrow + k0 + 8 * t) : half8{0, 0, 0, 0, 0, 0, 0, 0};
+        for (int j = 0; j < GPL; ++j) {
+            const int k0 = ((first + j) * kTileGroups + quarter) * kGroup;
+            const bool ok = m_ok[mb] && first + j < steps;
+            if constexpr (XL != 0) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    a[mb][j][t] = ok ? *reinterpret_cast<const half8*>(xsrow[mb] + k0 + 8 * t)
+                                     : half8{0, 0, 0, 0, 0, 0, 0, 0};
+                }
+            } else if (ok) {
+                load_x32(xrow[mb], k0, m.cols, xvec != 0, a[mb][j]);
+            } else {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) a[mb][j][t] = half8{0, 0, 0, 0, 0, 0, 0, 0};
             }
-        } else if (ok) {
-            load_x32(xrow, k0, m.cols, xvec != 0, a[j]);
-        } else {
-#pragma unroll
-            for (int t = 0; t < 4; ++t) a[j][t] = half8{0, 0, 0, 0, 0, 0, 0, 0};
         }
     }
 }
 
 // Decode the batch held in `cur` and accumulate it against `a`.
-template <int B, int MODE, int GPL, typename Bits>
-__device__ __forceinline__ void decode_mul_batch(const Bits (&cur)[GPL], const half8 (&a)[GPL][4], int first,
-                                                 int steps, float s, floatx4& acc) {
+// Decode the batch held in `cur` once and accumulate it against every
+// activation block.
+template <int B, int MODE, int GPL, int MB, typename Bits>
+__device__ __forceinline__ void decode_mul_batch(const Bits (&cur)[GPL], const half8 (&a)[MB][GPL][4], int first,
+                                                 int steps, float s, floatx4 (&acc)[MB]) {
 #pragma unroll
     for (int j = 0; j < GPL; ++j) {
         const bool st_ok = first + j < steps;
@@ -596,7 +603,9 @@ __device__ __forceinline__ void decode_mul_batch(const Bits (&cur)[GPL], const h
             if constexpr (MODE == kModeRaw) {
                 if (!st_ok) b = half8{0, 0, 0, 0, 0, 0, 0, 0};
             }
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j][t], b, acc, 0, 0, 0);
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+                acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mb][j][t], b, acc[mb], 0, 0, 0);
         }
     }
 }
@@ -622,7 +631,7 @@ __device__ __forceinline__ int select_matrix(const MultiTail& mt, DevMatrix& m, 
     return tile;
 }
 
-template <int B, int MODE, int WAVES, int GPL, int XL>
+template <int B, int MODE, int WAVES, int GPL, int XL, int MB>
 __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
     DevMatrix m, const uint16_t* __restrict__ x, int M, uint16_t* __restrict__ y,
     const uint16_t* __restrict__ bias, int xvec, const MultiTail mt) {
@@ -641,7 +650,9 @@ __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
     const int nl = lane & 15;
     const int quarter = lane >> 4;
     const int row = tile * kTileRows + nl;
-    const bool m_ok = nl < M;                        // activation row of the A operand
+    bool m_ok[MB];                                   // activation row 16 mb + nl of the A operand
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) m_ok[mb] = 16 * mb + nl < M;
     const int steps = m.spr;
     const int kpad = steps * kTileGroups * kGroup;
     float s = 0.0f;
@@ -693,12 +704,20 @@ __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
     // Steps past the end (steps % kBatch != 0) reload the last tile; they
     // meet zero activations, and raw fp16 weights, which could hold Inf or
     // NaN, are zeroed there.
-    floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    floatx4 acc[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[mb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     Bits buf0[GPL], buf1[GPL];
     const int nb = (steps + kBatch - 1) / kBatch;    // workgroup batches
-    const uint16_t* xrow = x + static_cast<size_t>(m_ok ? nl : 0) * m.cols;
-    const uint16_t* xsrow = xs + static_cast<size_t>(m_ok ? nl : 0) * kpad;
-    half8 a[GPL][4];
+    const uint16_t* xrow[MB];
+    const uint16_t* xsrow[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+        const int r = m_ok[mb] ? 16 * mb + nl : 0;
+        xrow[mb] = x + static_cast<size_t>(r) * m.cols;
+        xsrow[mb] = xs + static_cast<size_t>(r) * kpad;
+    }
+    half8 a[MB][GPL][4];
 
     // One batch is prefetched while the previous one is multiplied (two
     // register buffers alternate, so no register copy waits on loads in
@@ -724,9 +743,9 @@ __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
         }
     }
     auto batch = [&](const Bits (&cur)[GPL], Bits (&nxt)[GPL], bool prefetch, int bi) {
-        decode_activations<GPL, XL>(a, m, bi * kBatch, wave, quarter, m_ok, steps, xrow, xsrow, xvec);
+        decode_activations<GPL, XL, MB>(a, m, bi * kBatch, wave, quarter, m_ok, steps, xrow, xsrow, xvec);
         if (prefetch) decode_load_batch<GPL>(m, nxt, slot0, (bi + 1) * kBatch + wave * GPL, steps);
-        decode_mul_batch<B, MODE, GPL>(cur, a, bi * kBatch + wave * GPL, steps, s, acc);
+        decode_mul_batch<B, MODE, GPL, MB>(cur, a, bi * kBatch + wave * GPL, steps, s, acc);
     };
     for (int bi = 0;; bi += 2) {
         if (bi + 1 >= nb) {
@@ -741,20 +760,24 @@ __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
         batch(buf1, buf0, true, bi + 1);
     }
 
-    // cross-wave reduction of the 16x16 fp32 tile
+    // cross-wave reduction of each 16x16 fp32 block, one block at a time
     __shared__ floatx4 red[WAVES][64];
-    red[wave][lane] = acc;
-    __syncthreads();
-    if (threadIdx.x < 256) {
-        const int src = threadIdx.x & 63;
-        const int e = threadIdx.x >> 6;
-        float v = 0.0f;
 #pragma unroll
-        for (int w = 0; w < WAVES; ++w) v += red[w][src][e];
-        const int mi = 4 * (src >> 4) + e;           // D[4*(l/16)+e][l%16]
-        if (mi < M && on < m.rows) {
-            y[static_cast<size_t>(mi) * m.rows + on] =
-                epilogue<MODE>(v, out_scale, bias != nullptr, out_bias);
+    for (int mb = 0; mb < MB; ++mb) {
+        if (mb > 0) __syncthreads();
+        red[wave][lane] = acc[mb];
+        __syncthreads();
+        if (threadIdx.x < 256) {
+            const int src = threadIdx.x & 63;
+            const int e = threadIdx.x >> 6;
+            float v = 0.0f;
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) v += red[w][src][e];
+            const int mi = 16 * mb + 4 * (src >> 4) + e;   // D[4*(l/16)+e][l%16] of block mb
+            if (mi < M && on < m.rows) {
+                y[static_cast<size_t>(mi) * m.rows + on] =
+                    epilogue<MODE>(v, out_scale, bias != nullptr, out_bias);
+            }
         }
     }
 }
@@ -1818,7 +1841,12 @@ constexpr int kPrefillMI = EBK_PREFILL_MI;
 constexpr int kPrefillKS = EBK_PREFILL_KS;
 constexpr int kDecodeWaves = EBK_DECODE_WAVES;
 constexpr int kDecodeGpl = EBK_DECODE_GPL;
-constexpr int kDecodeMaxM = 16;
+// Activation rows the decode kernel takes (in blocks of 16; above, the
+// prefill kernels).
+#ifndef EBK_DECODE_MAX_M
+#define EBK_DECODE_MAX_M 64
+#endif
+constexpr int kDecodeMaxM = EBK_DECODE_MAX_M;
 // Modes the GEMV kernel takes (bit per Mode).  The decoded-fp16 mode
 // (b >= 11, fullPrecision) spends ~7 VALU instructions per code on the fp32
 // product and its rounding; at four waves per SIMD that work is exposed, and
@@ -1872,6 +1900,45 @@ inline bool prefer_wide_tiles(int64_t M, int rows, int cus) {
     return t_wide < t_narrow;
 }
 
+// Whether linear_decode_kernel finishes 16 < M <= kDecodeMaxM rows before
+// the prefill kernels.  The decode kernel reads the weights once, but every
+// row tile re-reads all M x K activations from L2; the 128-row prefill
+// tiles are few at these M, so their time is one tile's walk over K per
+// round.  Fitted on MI355X at b = 10 (us): decode ~ max(weight bytes at
+// 5 TB/s, rtiles * M * K * 2 at 6.5 TB/s) + 2; prefill ~ (3.5 + 0.0067 K)
+// per round (4096 x 4096: M = 64 decode 19.8 against prefill 35.1;
+// 11008 x 4096: M = 32 30.1 against 34.1, M = 64 54.9 against 38.0).
+inline bool prefer_decode(int64_t M, const DevMatrix& m, int cus) {
+    if (M <= 16) return true;
+    if (M > kDecodeMaxM) return false;
+    const double wbytes = static_cast<double>(m.rows) * m.cols * (m.bits == 16 ? 16 : m.bits) / 8.0;
+    const double xbytes = static_cast<double>(m.rtiles) * static_cast<double>(M) * m.cols * 2.0;
+    const double t_decode = std::max(wbytes / 5.0e6, xbytes / 6.5e6) + 2.0;
+    const int64_t tiles = 2 * ((m.rows + kPN - 1) / kPN);          // 128 x 128 halves at one M block
+    const double rounds = static_cast<double>((tiles + cus - 1) / cus);
+    const double t_prefill = (3.5 + 0.0067 * m.cols) * rounds;
+    return t_decode < t_prefill;
+}
+
+// linear_decode_kernel for M <= 16 MB rows: activations staged in LDS when
+// they fit (directly up to kXLdsDirectBytes when x's rows are whole tiles),
+// read per lane from L2 otherwise.
+template <int B, int MODE, int MB>
+void launch_decode(const DevMatrix& m, const uint16_t* x, int64_t M, uint16_t* y, const uint16_t* bias, int xvec,
+                   hipStream_t s, const MultiTail& mt, int tiles) {
+    const size_t xbytes = static_cast<size_t>(M) * m.spr * kTileGroups * kGroup * 2;
+    if (xbytes <= static_cast<size_t>(kXLdsBytes)) {
+        hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, 1, MB>), dim3(tiles),
+                           dim3(64 * kDecodeWaves), xbytes, s, m, x, static_cast<int>(M), y, bias, xvec, mt);
+    } else if (xvec == 2 && xbytes <= static_cast<size_t>(kXLdsDirectBytes)) {
+        hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, 2, MB>), dim3(tiles),
+                           dim3(64 * kDecodeWaves), xbytes, s, m, x, static_cast<int>(M), y, bias, xvec, mt);
+    } else {
+        hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, 0, MB>), dim3(tiles),
+                           dim3(64 * kDecodeWaves), 0, s, m, x, static_cast<int>(M), y, bias, xvec, mt);
+    }
+}
+
 // mt: the other matrices of a multi-matrix decode launch (count 1 for a
 // single matrix; only M <= kDecodeMaxM takes more than one).
 template <int B, int MODE>
@@ -1888,17 +1955,13 @@ hipError_t run_linear_mode(const DevMatrix& m, const uint16_t* x, int64_t M, uin
     if (M == 1 && xvec == 2 && gemv_takes<B, MODE>(m)) {
         hipLaunchKernelGGL((linear_gemv_kernel<B, MODE>), dim3(tiles), dim3(64 * kGemvWaves),
                            static_cast<size_t>(m.cols) * 2, s, m, x, y, bias, mt);
-    } else if (M <= kDecodeMaxM) {
-        const size_t xbytes = static_cast<size_t>(M) * m.spr * kTileGroups * kGroup * 2;
-        if (xbytes <= static_cast<size_t>(kXLdsBytes)) {
-            hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, 1>), dim3(tiles),
-                               dim3(64 * kDecodeWaves), xbytes, s, m, x, static_cast<int>(M), y, bias, xvec, mt);
-        } else if (xvec == 2 && xbytes <= static_cast<size_t>(kXLdsDirectBytes)) {
-            hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, 2>), dim3(tiles),
-                               dim3(64 * kDecodeWaves), xbytes, s, m, x, static_cast<int>(M), y, bias, xvec, mt);
-        } else {
-            hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, 0>), dim3(tiles),
-                               dim3(64 * kDecodeWaves), 0, s, m, x, static_cast<int>(M), y, bias, xvec, mt);
+    } else if (M <= 16 || (M <= kDecodeMaxM && (mt.count > 1 || prefer_decode(M, m, device_cu_count())))) {
+        if (M <= 16) {
+            launch_decode<B, MODE, 1>(m, x, M, y, bias, xvec, s, mt, tiles);
+        } else if (M <= 32) {
+            launch_decode<B, MODE, 2>(m, x, M, y, bias, xvec, s, mt, tiles);
+        } else if constexpr (kDecodeMaxM > 32) {
+            launch_decode<B, MODE, 4>(m, x, M, y, bias, xvec, s, mt, tiles);
         }
     } else if (mt.count > 1) {
         return hipErrorInvalidValue;      // the launcher splits prefill per matrix
@@ -2020,7 +2083,9 @@ hipError_t launch_linear_multi(const DevMatrix* ms, int count, bool exact_w16, c
     for (int j = 1; j < count; ++j) {
         if (ms[j].cols != ms[0].cols || ms[j].bits != ms[0].bits) return hipErrorInvalidValue;
     }
-    if (M > kDecodeMaxM) {
+    bool fused = M <= kDecodeMaxM;
+    for (int j = 0; j < count && fused; ++j) fused = prefer_decode(M, ms[j], device_cu_count());
+    if (!fused) {
         for (int j = 0; j < count; ++j) {
             const hipError_t e = run_linear(ms[j], exact_w16, x, M, ys[j], biases ? biases[j] : nullptr, stream,
                                             MultiTail{});

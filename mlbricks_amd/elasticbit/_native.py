@@ -208,7 +208,8 @@ def forward_torch_multi(matrices: Sequence["RuntimeMatrix"], input: torch.Tensor
     """``[m.forwardTorch(input, bias=b) for m, b in zip(matrices, biases)]``
     in as few launches as the widths allow: matrices that read the same
     activations (a QKV or Gate/Up group) share one decode launch for up to
-    16 rows of ``input``.  Every matrix must have ``cols`` equal to the last
+    16 rows of ``input`` (64 where the decode kernel is the faster route for
+    each matrix).  Every matrix must have ``cols`` equal to the last
     dimension of ``input`` and live on its device.  No single-call
     counterpart in the reference, whose Stage-2F concatenates the
     materialized weights instead (stage2f.py:382-420)."""

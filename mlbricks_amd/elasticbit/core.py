@@ -14,8 +14,8 @@ as bit planes, still b bits per weight -- and decodes them in registers:
   scale once; b >= 13 uses the decoded fp16 weights fp16_rn(q*s) (W16A16
   arithmetic, as the reference does for b >= 9);
 * ``fullPrecision``: every width uses the decoded fp16 weights;
-* one fused kernel family serves decode (M <= 16) and prefill (M > 16) on the
-  matrix cores; activations stay fp16 everywhere.
+* one fused kernel family serves decode (M <= 16, and up to 64 where it is
+  faster) and prefill on the matrix cores; activations stay fp16 everywhere.
 
 ``_ElasticLinear`` routes through the execution planner: ``backend='auto'``
 qualifies the HIP route against the PyTorch route (materialize + F.linear)
@@ -276,7 +276,8 @@ class RuntimeMatrix:
                           biases: Sequence[torch.Tensor | None] | None = None) -> list[torch.Tensor]:
         """``[m.forward(x) (+ bias) for m in matrices]`` for matrices that read
         the same fp16 CUDA activations, in one decode launch per run of equal
-        widths (up to four matrices, up to 16 activation rows).  No
+        widths (up to four matrices; up to 16 activation rows, or 64 where the
+        decode kernel is the faster route).  No
         single-call counterpart in the reference (its Stage-2F concatenates
         the materialized weights, stage2f.py:382-420)."""
         native = _requireNative()

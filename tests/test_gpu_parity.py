@@ -234,11 +234,12 @@ def test_fp16_fallback_prefill_ragged(native, rows, cols, M, tiles):
     assert _rel_max(y, ref) <= TOL
 
 
-@pytest.mark.parametrize("M", [2, 4, 8, 16])
+@pytest.mark.parametrize("M", [2, 4, 8, 16, 24, 40, 64])
 @pytest.mark.parametrize("cols,aligned", [(4096, True), (4608, True), (11008, True), (1000, True), (4096, False)])
 @pytest.mark.parametrize("b", [8, 10, 13])
 def test_decode_activation_staging(native, M, cols, aligned, b):
-    """M <= 16 decode over the three activation paths: staged in LDS up to
+    """M <= 64 decode (one, two or four 16-row activation blocks per decoded
+    weight operand) over the three activation paths: staged in LDS up to
     32 KB (direct or through registers), staged directly up to 144 KB (16 x
     4608 exactly) when x rows are whole 128-column tiles and 16-byte aligned,
     read per lane from global memory otherwise -- with ragged K and an
