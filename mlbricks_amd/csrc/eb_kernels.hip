@@ -1074,10 +1074,10 @@ template <int MI>
 struct PrefillShape {
     // 256 rows (MI = 8) needs 256 accumulator registers per lane; that build
     // spilled and did not reproduce the oracle, so only 128 rows is enabled.
-    static_assert(MI == 4, "the prefill kernel is built for 128 activation rows per workgroup");
+    static_assert(MI == 4 || MI == 2, "the prefill kernel is built for 128 or 64 activation rows per workgroup");
     static constexpr int kRows = 32 * MI;            // activation rows per workgroup
     static constexpr int kStage = kRows * kPRow;     // bytes per activation stage
-    static constexpr int kStages = MI == 4 ? 3 : 2;  // 96 KB or 128 KB of LDS
+    static constexpr int kStages = MI <= 4 ? 3 : 2;  // 48 KB, 96 KB or 128 KB of LDS
     static constexpr int kLds = kStages * kStage;
     static constexpr int kALoads = kRows / 16;       // A loads per step per wave (1 KB each)
     static constexpr int kADist = kStages - 1;       // activation prefetch distance
@@ -1151,11 +1151,14 @@ __global__ __launch_bounds__(256 * KS) void linear_prefill_kernel(
     // M * cols * 2 below 4 GiB.
     // Instruction i covers rows w*Shape::kRows/4 + 4i + l/16; its chunk pattern
     // repeats every four instructions.
-    int achunk[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) achunk[i] = 8 * ((lane & 15) ^ ((4 * i + (lane >> 4)) & 15));
     constexpr int kAWaveRows = Shape::kRows / (4 * KS);   // rows each wave loads
     constexpr int kAWaveLoads = kAWaveRows / 4;          // 1 KB instructions per wave
+    // swizzle of row wave_id * kAWaveRows + 4i + l/16 (not a multiple of 16
+    // apart for every wave when kAWaveRows < 16)
+    int achunk[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        achunk[i] = 8 * ((lane & 15) ^ ((wave_id * kAWaveRows + 4 * i + (lane >> 4)) & 15));
     const int arow0 = m0 + wave_id * kAWaveRows + (lane >> 4);
     const uint8_t* xb = reinterpret_cast<const uint8_t*>(x);
     auto load_a = [&](int st, int stage) {
@@ -1306,26 +1309,31 @@ __global__ __launch_bounds__(256 * KS) void linear_prefill_kernel(
     __syncthreads();
     if constexpr (KS == 2) {
         // The K-half-1 waves hand their partial sums to the K-half-0 waves
-        // of the same column group through LDS, two row blocks at a time.
-        float* red = reinterpret_cast<float*>(xs) + wave * (2 * NB * 16 * 64);
+        // of the same column group through LDS, kRB row blocks at a time
+        // (two when the four column groups' 4 * kRB * NB * 4 KB fit).
+        constexpr int kRB = 4 * 2 * NB * 16 * 64 * 4 <= Shape::kLds ? 2 : 1;
+        static_assert(4 * kRB * NB * 16 * 64 * 4 <= Shape::kLds, "K-split reduction exceeds the activation LDS");
+        float* red = reinterpret_cast<float*>(xs) + wave * (kRB * NB * 16 * 64);
 #pragma unroll
-        for (int h = 0; h < MI / 2; ++h) {
+        for (int h = 0; h < MI / kRB; ++h) {
             if (kp == 1) {
 #pragma unroll
-                for (int i2 = 0; i2 < 2; ++i2)
+                for (int i2 = 0; i2 < kRB; ++i2)
 #pragma unroll
                     for (int nb2 = 0; nb2 < NB; ++nb2)
 #pragma unroll
-                        for (int e = 0; e < 16; ++e) red[((i2 * NB + nb2) * 16 + e) * 64 + lane] = acc[2 * h + i2][nb2][e];
+                        for (int e = 0; e < 16; ++e)
+                            red[((i2 * NB + nb2) * 16 + e) * 64 + lane] = acc[kRB * h + i2][nb2][e];
             }
             __syncthreads();
             if (kp == 0) {
 #pragma unroll
-                for (int i2 = 0; i2 < 2; ++i2)
+                for (int i2 = 0; i2 < kRB; ++i2)
 #pragma unroll
                     for (int nb2 = 0; nb2 < NB; ++nb2)
 #pragma unroll
-                        for (int e = 0; e < 16; ++e) acc[2 * h + i2][nb2][e] += red[((i2 * NB + nb2) * 16 + e) * 64 + lane];
+                        for (int e = 0; e < 16; ++e)
+                            acc[kRB * h + i2][nb2][e] += red[((i2 * NB + nb2) * 16 + e) * 64 + lane];
             }
             __syncthreads();
         }
@@ -1333,7 +1341,8 @@ __global__ __launch_bounds__(256 * KS) void linear_prefill_kernel(
     constexpr int kCols = 32 * NB;               // output columns per wave
     constexpr int kTileCols = 4 * kCols;         // output columns per workgroup
     constexpr int kCPitch = 2 * kTileCols + 16;  // bytes per staged output row
-    constexpr int kCRows = 128;                  // rows per pass
+    constexpr int kPassBlocks = MI < 4 ? MI : 4; // 32-row blocks per output pass
+    constexpr int kCRows = 32 * kPassBlocks;     // rows per pass
     constexpr int kLanesPerRow = kTileCols / 8;  // 16-byte chunks per row
     constexpr int kThreads = 256 * KS;
     static_assert(kCRows * kCPitch <= Shape::kLds, "output staging exceeds the activation LDS");
@@ -1350,7 +1359,7 @@ __global__ __launch_bounds__(256 * KS) void linear_prefill_kernel(
     const bool yvec = (m.rows % 8 == 0) && (reinterpret_cast<uintptr_t>(y) % 16 == 0);
     const int chunk = threadIdx.x % kLanesPerRow;
 #pragma unroll
-    for (int pass = 0; pass < MI / 4; ++pass) {
+    for (int pass = 0; pass < MI / kPassBlocks; ++pass) {
         if (pass > 0) __syncthreads();
         // the whole workgroup tile goes to LDS so that rows leave as
         // contiguous 2*kTileCols-byte segments
@@ -1359,12 +1368,13 @@ __global__ __launch_bounds__(256 * KS) void linear_prefill_kernel(
 #pragma unroll
             for (int nb2 = 0; nb2 < NB; ++nb2) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
+                for (int i = 0; i < kPassBlocks; ++i) {
 #pragma unroll
                     for (int e = 0; e < 16; ++e) {
                         const int r = 32 * i + 8 * (e >> 2) + 4 * half + (e & 3);
                         *reinterpret_cast<uint16_t*>(cw + r * kCPitch + (32 * nb2 + n32) * 2) =
-                            epilogue<MODE>(acc[4 * pass + i][nb2][e], sn[nb2], bias != nullptr, bn[nb2]);
+                            epilogue<MODE>(acc[kPassBlocks * pass + i][nb2][e], sn[nb2], bias != nullptr,
+                                           bn[nb2]);
                     }
                 }
             }
@@ -1382,7 +1392,10 @@ __global__ __launch_bounds__(256 * KS) void linear_prefill_kernel(
                 *reinterpret_cast<uint4*>(dst) = v;
             } else {
                 const uint16_t* h = reinterpret_cast<const uint16_t*>(&v);
-                for (int k = 0; k < 8 && gn + k < m.rows; ++k) dst[k] = h[k];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    if (gn + k < m.rows) dst[k] = h[k];
+                }
             }
         }
     }
@@ -1679,7 +1692,10 @@ __global__ __launch_bounds__(256) void linear_prefill_wide_kernel(
                 *reinterpret_cast<uint4*>(dst) = v;
             } else {
                 const uint16_t* hh = reinterpret_cast<const uint16_t*>(&v);
-                for (int k = 0; k < 8 && gn + k < m.rows; ++k) dst[k] = hh[k];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    if (gn + k < m.rows) dst[k] = hh[k];
+                }
             }
         }
     }
@@ -1900,24 +1916,70 @@ inline bool prefer_wide_tiles(int64_t M, int rows, int cus) {
     return t_wide < t_narrow;
 }
 
+// Tiles of linear_prefill_kernel with MI 32-row activation blocks: full
+// tiles are 32 MI x 256; when the last round of full tiles would leave at
+// least half the CUs idle, its tiles run as two 32 MI x 128 halves instead,
+// so it takes half a round.  Returns the full tiles to launch of `tiles`.
+inline int narrow_full_tiles(int tiles, int cus) {
+    if (tiles <= cus / 2) return 0;
+    if (tiles % cus != 0 && tiles % cus <= cus / 2) return tiles - tiles % cus;
+    return tiles;
+}
+
+// Workgroups linear_prefill_kernel launches for M rows at MI.
+inline int narrow_workgroups(int64_t M, int rows, int mi, int cus) {
+    const int tiles = static_cast<int>((M + 32 * mi - 1) / (32 * mi)) * ((rows + kPN - 1) / kPN);
+    const int full = narrow_full_tiles(tiles, cus);
+    return full + 2 * (tiles - full);
+}
+
 // Whether linear_decode_kernel finishes 16 < M <= kDecodeMaxM rows before
-// the prefill kernels.  The decode kernel reads the weights once, but every
-// row tile re-reads all M x K activations from L2; the 128-row prefill
-// tiles are few at these M, so their time is one tile's walk over K per
-// round.  Fitted on MI355X at b = 10 (us): decode ~ max(weight bytes at
-// 5 TB/s, rtiles * M * K * 2 at 6.5 TB/s) + 2; prefill ~ (3.5 + 0.0067 K)
-// per round (4096 x 4096: M = 64 decode 19.8 against prefill 35.1;
-// 11008 x 4096: M = 32 30.1 against 34.1, M = 64 54.9 against 38.0).
+// the prefill kernel.  The decode kernel reads the weights once, but every
+// row tile re-reads all M x K activations from L2; the 64-row prefill tiles
+// are few at these M, so their time is one tile's walk over K per round.
+// Fitted on MI355X at b = 10 (us): decode ~ max(weight bytes at 5 TB/s,
+// rtiles * M * K * 2 at 6.5 TB/s) + 2; prefill ~ (3 + 0.005 K) per round
+// (4096 x 4096 M = 64: decode 19.8 against prefill ~24; 11008 x 4096
+// M = 32: decode 30.2 against prefill ~25).
 inline bool prefer_decode(int64_t M, const DevMatrix& m, int cus) {
     if (M <= 16) return true;
     if (M > kDecodeMaxM) return false;
     const double wbytes = static_cast<double>(m.rows) * m.cols * (m.bits == 16 ? 16 : m.bits) / 8.0;
     const double xbytes = static_cast<double>(m.rtiles) * static_cast<double>(M) * m.cols * 2.0;
     const double t_decode = std::max(wbytes / 5.0e6, xbytes / 6.5e6) + 2.0;
-    const int64_t tiles = 2 * ((m.rows + kPN - 1) / kPN);          // 128 x 128 halves at one M block
-    const double rounds = static_cast<double>((tiles + cus - 1) / cus);
-    const double t_prefill = (3.5 + 0.0067 * m.cols) * rounds;
+    const int wgs = narrow_workgroups(M, m.rows, 2, cus);
+    const double rounds = static_cast<double>((wgs + cus - 1) / cus);
+    const double t_prefill = (3.0 + 0.005 * m.cols) * rounds;
     return t_decode < t_prefill;
+}
+
+// linear_prefill_kernel with MI = 4 (128-row tiles) or, where those would
+// keep at most half the CUs busy, MI = 2 (64-row tiles).  Measured on MI355X
+// at b = 10 (us, 128-row -> 64-row tiles): 4096 x 4096 M = 128..512
+// 35 -> 24; 4096 x 11008 M = 128 88 -> 59; 1024 x 1024 M = 512 12.1 -> 8.1;
+// with more tiles the 128-row tiles win (11008 x 4096 M = 512: 58.5
+// against 65).
+template <int B, int MODE, int MI>
+void launch_narrow(const DevMatrix& m, const uint16_t* x, int64_t M, uint16_t* y, const uint16_t* bias,
+                   hipStream_t s, int cus) {
+    constexpr int kRows = 32 * MI;
+    const int mblocks = static_cast<int>((M + kRows - 1) / kRows);
+    const int nblocks = (m.rows + kPN - 1) / kPN;
+    const int tiles = mblocks * nblocks;
+    const int full = narrow_full_tiles(tiles, cus);
+    if (full > 0) {
+        const int per_xcd = (full + 7) / 8;
+        hipLaunchKernelGGL((linear_prefill_kernel<B, MODE, MI, 2, kPrefillKS>), dim3(8 * per_xcd),
+                           dim3(256 * kPrefillKS), 0, s, m, x, static_cast<int>(M), y, bias, mblocks, nblocks, 0,
+                           full, per_xcd);
+    }
+    if (full < tiles) {
+        const int jobs = 2 * (tiles - full);
+        const int per_xcd = (jobs + 7) / 8;
+        hipLaunchKernelGGL((linear_prefill_kernel<B, MODE, MI, 1, kPrefillKS>), dim3(8 * per_xcd),
+                           dim3(256 * kPrefillKS), 0, s, m, x, static_cast<int>(M), y, bias, mblocks, nblocks,
+                           full, jobs, per_xcd);
+    }
 }
 
 // linear_decode_kernel for M <= 16 MB rows: activations staged in LDS when
@@ -1978,32 +2040,11 @@ hipError_t run_linear_mode(const DevMatrix& m, const uint16_t* x, int64_t M, uin
         }
     } else if ((MODE != kModeRaw || EBK_PREFILL_RAW) && xvec && offsets32) {
         if constexpr (MODE != kModeRaw || EBK_PREFILL_RAW) {
-            // Full tiles are 128 x 256.  When the last round of full tiles
-            // would leave at least half the CUs idle, its tiles run as two
-            // 128 x 128 halves instead, so it takes half a round.
-            constexpr int kRows = 32 * kPrefillMI;
-            const int mblocks = static_cast<int>((M + kRows - 1) / kRows);
-            const int nblocks = (m.rows + kPN - 1) / kPN;
-            const int tiles = mblocks * nblocks;
             const int cus = device_cu_count();
-            int full = tiles;
-            if (tiles <= cus / 2) {
-                full = 0;
-            } else if (tiles % cus != 0 && tiles % cus <= cus / 2) {
-                full = tiles - tiles % cus;
-            }
-            if (full > 0) {
-                const int per_xcd = (full + 7) / 8;
-                hipLaunchKernelGGL((linear_prefill_kernel<B, MODE, kPrefillMI, 2, kPrefillKS>), dim3(8 * per_xcd),
-                                   dim3(256 * kPrefillKS), 0, s, m, x, static_cast<int>(M), y, bias, mblocks, nblocks, 0,
-                                   full, per_xcd);
-            }
-            if (full < tiles) {
-                const int jobs = 2 * (tiles - full);
-                const int per_xcd = (jobs + 7) / 8;
-                hipLaunchKernelGGL((linear_prefill_kernel<B, MODE, kPrefillMI, 1, kPrefillKS>), dim3(8 * per_xcd),
-                                   dim3(256 * kPrefillKS), 0, s, m, x, static_cast<int>(M), y, bias, mblocks, nblocks,
-                                   full, jobs, per_xcd);
+            if (narrow_workgroups(M, m.rows, 4, cus) <= cus / 2) {
+                launch_narrow<B, MODE, 2>(m, x, M, y, bias, s, cus);
+            } else {
+                launch_narrow<B, MODE, 4>(m, x, M, y, bias, s, cus);
             }
         }
     } else {

@@ -582,6 +582,21 @@ def test_prefill_tiling_shapes_match_decoded_product(native, rows, cols, M, b, p
         native.set_prefill_tiles("auto")
 
 
+# Grids small enough that the 128-row prefill tiles would keep at most half
+# of a 256-CU GPU busy, so the prefill runs 64-row tiles; M ragged against
+# 64, K ragged against 128, b from 4 to 15 in both arithmetics.
+@pytest.mark.parametrize("rows,cols,M,b,policy", [
+    (4096, 1000, 96, 10, "hardwareNative"),
+    (1000, 2048, 300, 4, "hardwareNative"),
+    (520, 4096, 130, 13, "hardwareNative"),
+    (2900, 776, 65, 9, "fullPrecision"),
+    (1536, 384, 256, 8, "hardwareNative"),
+    (4096, 1024, 200, 15, "fullPrecision"),
+])
+def test_prefill_small_grids_match_decoded_product(native, rows, cols, M, b, policy):
+    _check_prefill_shape(native, rows, cols, M, b, policy)
+
+
 def _check_prefill_shape(native, rows, cols, M, b, policy):
     rng = np.random.default_rng(rows + cols + M + b)
     q = _codes(rng, rows, cols, b)
