@@ -1775,17 +1775,18 @@ __global__ void packed_linear_kernel(const void* __restrict__ x, int x_dtype, in
 // dispatch helpers
 // ---------------------------------------------------------------------------
 
-// Compute units of the current device, cached per device.
+// Compute units of the current device, cached per device (threads may race
+// to fill an entry; they store the same value).
 int device_cu_count() {
-    static int cached[64] = {};
+    static std::atomic<int> cached[64] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cached[dev] == 0) {
-        int n = 0;
+    int n = cached[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cached[dev] = n;
+        cached[dev].store(n, std::memory_order_relaxed);
     }
-    return cached[dev];
+    return n;
 }
 
 inline unsigned blocks_for(uint64_t n, unsigned threads) {
