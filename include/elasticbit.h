@@ -122,6 +122,16 @@ int eb_compress_selected_codes(const int16_t* codes, const float* scales, int ro
                                int selected_bits, double threshold, double selected_error,
                                int policy, eb_matrix** out);
 
+/* eb_compress_selected_codes with the codes in device memory (int16
+ * [rows][cols] on the current HIP device; scales on the host), as the GPU
+ * width search leaves them.  The canonical bitstream (pack_exact_codes,
+ * runtime.cu:150-186) is packed on the device and repacked there; only the
+ * packed stream, b bits per weight, is copied back for the matrix's host
+ * copy.  Same validation and errors as the host version.  Synchronous. */
+int eb_compress_selected_codes_device(const int16_t* codes_dev, const float* scales, int rows, int cols,
+                                      int selected_bits, double threshold, double selected_error,
+                                      int policy, eb_matrix** out);
+
 /* RuntimeMatrix.load, runtime.cu:810-871 (MLB4 reader). */
 int eb_load(const char* path, int policy, eb_matrix** out);
 

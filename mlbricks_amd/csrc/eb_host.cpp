@@ -506,7 +506,10 @@ struct eb_matrix {
     // Upload the canonical stream and re-lay it out as bit planes on the
     // current device (the reference widens at the same point,
     // configure_execution_weights, runtime.cu:1315-1334).
-    void build_device() {
+    // Execution layout on the current device, repacked from the canonical
+    // stream: `d_canon` when the caller already holds a device copy, else
+    // an upload of `payload`.
+    void build_device(const uint8_t* d_canon = nullptr) {
         if (!device_present()) return;
         EB_HIP(hipGetDevice(&device));
         const int gpr = (cols + ebk::kGroup - 1) / ebk::kGroup;
@@ -560,14 +563,19 @@ struct eb_matrix {
             dev.scales = d_scales;
         }
 
-        void* d_canon = nullptr;
-        EB_HIP(hipMalloc(&d_canon, std::max<size_t>(payload.size(), 1)));
-        hipError_t err = hipMemcpy(d_canon, payload.data(), payload.size(), hipMemcpyHostToDevice);
+        if (d_canon) {
+            EB_HIP(ebk::launch_repack(d_canon, payload.size(), out, nullptr));
+            EB_HIP(hipStreamSynchronize(nullptr));
+            return;
+        }
+        void* d_copy = nullptr;
+        EB_HIP(hipMalloc(&d_copy, std::max<size_t>(payload.size(), 1)));
+        hipError_t err = hipMemcpy(d_copy, payload.data(), payload.size(), hipMemcpyHostToDevice);
         if (err == hipSuccess) {
-            err = ebk::launch_repack(static_cast<const uint8_t*>(d_canon), payload.size(), out, nullptr);
+            err = ebk::launch_repack(static_cast<const uint8_t*>(d_copy), payload.size(), out, nullptr);
         }
         if (err == hipSuccess) err = hipStreamSynchronize(nullptr);
-        (void)hipFree(d_canon);
+        (void)hipFree(d_copy);
         EB_HIP(err);
     }
 
@@ -747,6 +755,64 @@ int eb_compress_selected_codes(const int16_t* codes, const float* scales, int ro
         std::vector<uint8_t> payload = pack_exact_codes(codes, static_cast<size_t>(rows) * cols, selected_bits);
         *out = make_matrix(rows, cols, selected_bits, threshold, selected_error, policy, std::move(s),
                            std::move(payload)).release();
+    });
+}
+
+int eb_compress_selected_codes_device(const int16_t* codes_dev, const float* scales, int rows, int cols,
+                                      int selected_bits, double threshold, double selected_error, int policy,
+                                      eb_matrix** out) {
+    return guarded([&] {                                 // runtime.cu:778-808, 150-186
+        require(codes_dev && scales && out, "compressSelectedCodes: null pointer");
+        validate_storage_bits(selected_bits);
+        if (selected_bits == kFallbackBits) {
+            throw std::invalid_argument("prequantized codes require 3..15-bit storage");
+        }
+        check_threshold(threshold);
+        if (!std::isfinite(selected_error) || selected_error < 0.0 || selected_error > threshold) {
+            throw std::invalid_argument("selected compressed width does not satisfy threshold");
+        }
+        parse_policy(policy);
+        check_dims(rows, cols);
+        require(device_present(), "ElasticBit requires its CUDA runtime: no HIP (gfx950) device is available");
+        std::vector<float> s(scales, scales + rows);
+        for (float v : s) {
+            if (!std::isfinite(v) || v <= 0.0f) {
+                throw std::invalid_argument("ElasticBit scales must be finite and positive");
+            }
+        }
+        const size_t count = static_cast<size_t>(rows) * cols;
+        const size_t nbytes = packed_bytes(count, selected_bits);
+        // one allocation: the stream, then the range flag (256-byte aligned)
+        const size_t flag_off = align_up(std::max<size_t>(nbytes, 1), 256);
+        void* d_buf = nullptr;
+        EB_HIP(hipMalloc(&d_buf, flag_off + sizeof(int)));
+        auto* d_canon = static_cast<uint8_t*>(d_buf);
+        auto* d_bad = reinterpret_cast<int*>(d_canon + flag_off);
+        std::unique_ptr<eb_matrix> m;
+        try {
+            EB_HIP(hipMemset(d_bad, 0, sizeof(int)));
+            EB_HIP(ebk::launch_pack_codes(codes_dev, count, selected_bits, d_canon, nbytes, d_bad, nullptr));
+            int bad = 0;
+            EB_HIP(hipMemcpy(&bad, d_bad, sizeof(int), hipMemcpyDeviceToHost));
+            if (bad) throw std::invalid_argument("prequantized ElasticBit code exceeds selected bit range");
+            std::vector<uint8_t> payload(nbytes);
+            EB_HIP(hipMemcpy(payload.data(), d_canon, nbytes, hipMemcpyDeviceToHost));
+            m = std::make_unique<eb_matrix>();
+            m->rows = rows;
+            m->cols = cols;
+            m->bits = selected_bits;
+            m->threshold = threshold;
+            m->selected_error = selected_error;
+            m->policy = policy;
+            m->scales = std::move(s);
+            m->payload = std::move(payload);
+            m->build_device(d_canon);
+        } catch (...) {
+            (void)hipFree(d_buf);
+            throw;
+        }
+        (void)hipFree(d_buf);
+        *out = m.release();
     });
 }
 

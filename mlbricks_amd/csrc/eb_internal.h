@@ -97,6 +97,12 @@ inline size_t plane_bytes(int bits, int width, size_t groups) {
     return groups * 4u * static_cast<size_t>(width);
 }
 
+// int16 codes (device) -> canonical bitstream (device), b = 3..15; *bad
+// (device, zeroed by the caller) becomes nonzero for a code outside
+// [-qmax, qmax].
+hipError_t launch_pack_codes(const int16_t* codes, uint64_t count, int bits, uint8_t* out, uint64_t out_bytes,
+                             int* bad, hipStream_t stream);
+
 // Canonical bitstream (device copy) -> bit planes.
 hipError_t launch_repack(const uint8_t* canon, uint64_t canon_bytes, const DevMatrixOut& out,
                          hipStream_t stream);

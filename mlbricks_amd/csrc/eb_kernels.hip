@@ -293,6 +293,40 @@ __global__ void repack_kernel(const uint8_t* __restrict__ canon, uint64_t canon_
     }
 }
 
+// Codes q (int16, row-major) -> the canonical LSB-first bitstream of
+// u = q + qmax (pack_exact_codes, runtime.cu:150-186).  Eight codes of B
+// bits fill exactly B bytes, so thread t writes bytes B t .. B t + B - 1
+// from codes 8t .. 8t + 7 (past the last code: u = 0, and no byte past the
+// stream).  A code outside [-qmax, qmax] sets *bad.
+template <int B>
+__global__ void pack_codes_kernel(const int16_t* __restrict__ codes, uint64_t count, uint8_t* __restrict__ out,
+                                  uint64_t out_bytes, int* __restrict__ bad) {
+    constexpr int kQmax = (1 << (B - 1)) - 1;
+    const uint64_t t = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const uint64_t i0 = 8 * t;
+    if (i0 >= count) return;
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+    bool ok = true;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        uint32_t u = 0u;
+        if (i0 + j < count) {
+            const int q = codes[i0 + j];
+            ok = ok && q >= -kQmax && q <= kQmax;
+            u = static_cast<uint32_t>(q + kQmax) & ((1u << B) - 1u);
+        }
+        const int p = j * B;                      // bit offset within the B bytes
+        w[p >> 5] |= u << (p & 31);
+        if ((p & 31) + B > 32) w[(p >> 5) + 1] |= u >> (32 - (p & 31));
+    }
+    if (!ok) atomicOr(bad, 1);
+    const uint64_t o = t * B;
+#pragma unroll
+    for (int k = 0; k < B; ++k) {
+        if (o + k < out_bytes) out[o + k] = static_cast<uint8_t>(w[k >> 2] >> (8 * (k & 3)));
+    }
+}
+
 __global__ void repack16_kernel(const uint16_t* __restrict__ canon, DevMatrixOut out, uint64_t slots) {
     const uint64_t g = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (g >= slots) return;
@@ -1824,6 +1858,17 @@ struct RepackOp {
 };
 
 template <int B>
+struct PackCodesOp {
+    static hipError_t run(const int16_t* codes, uint64_t count, uint8_t* out, uint64_t out_bytes, int* bad,
+                          hipStream_t s) {
+        const uint64_t chunks = (count + 7) / 8;
+        hipLaunchKernelGGL(pack_codes_kernel<B>, dim3(blocks_for(chunks, 256)), dim3(256), 0, s, codes, count, out,
+                           out_bytes, bad);
+        return hipGetLastError();
+    }
+};
+
+template <int B>
 struct UnpackOp {
     static hipError_t run(const DevMatrix& m, int16_t* out, hipStream_t s) {
         const uint64_t slots = static_cast<uint64_t>(m.rtiles) * m.spr * kTileSlots;
@@ -2085,6 +2130,11 @@ hipError_t launch_repack(const uint8_t* canon, uint64_t canon_bytes, const DevMa
 }
 
 void set_prefill_tiles(int mode) { g_prefill_tiles.store(mode, std::memory_order_relaxed); }
+
+hipError_t launch_pack_codes(const int16_t* codes, uint64_t count, int bits, uint8_t* out, uint64_t out_bytes,
+                             int* bad, hipStream_t stream) {
+    return dispatch_bits<PackCodesOp>(bits, codes, count, out, out_bytes, bad, stream);
+}
 
 hipError_t launch_unpack(const DevMatrix& m, int16_t* out, hipStream_t stream) {
     return dispatch_bits<UnpackOp>(m.bits, m, out, stream);

@@ -85,6 +85,7 @@ _sig("eb_backend_info", [ctypes.POINTER(_Backend)])
 _sig("eb_compress", [_f32p, _i, _i, _f32p, _i, _d, _i, ctypes.POINTER(_vp)])
 _sig("eb_compress_selected", [_f32p, _i, _i, _i, _d, _d, _i, ctypes.POINTER(_vp)])
 _sig("eb_compress_selected_codes", [_i16p, _f32p, _i, _i, _i, _d, _d, _i, ctypes.POINTER(_vp)])
+_sig("eb_compress_selected_codes_device", [_vp, _f32p, _i, _i, _i, _d, _d, _i, ctypes.POINTER(_vp)])
 _sig("eb_load", [ctypes.c_char_p, _i, ctypes.POINTER(_vp)])
 _sig("eb_save", [_vp, ctypes.c_char_p])
 _sig("eb_destroy", [_vp], None)
@@ -386,6 +387,26 @@ class RuntimeMatrix:
         check(_lib.eb_compress_selected_codes(_ptr(q, ctypes.c_int16), _ptr(s, ctypes.c_float), q.shape[0],
                                               q.shape[1], int(selectedBits), float(threshold),
                                               float(selectedError), _policy(decodePolicy), ctypes.byref(h)))
+        return RuntimeMatrix(h)
+
+    @staticmethod
+    def _compressSelectedCodesTorch(codes: torch.Tensor, scales: Any, selectedBits: int, threshold: float,
+                                    selectedError: float, decodePolicy: str = "hardwareNative") -> "RuntimeMatrix":
+        """_compressSelectedCodes for int16 codes already on the HIP device
+        (the GPU width search's output): packed and repacked on the device,
+        only the b-bit stream comes back to the host copy."""
+        if not torch.is_tensor(codes) or not codes.is_cuda or codes.dtype != torch.int16 or codes.dim() != 2:
+            raise ValueError("codes must be a 2D int16 CUDA tensor")
+        q = codes.contiguous()
+        s = np.ascontiguousarray(scales, dtype=np.float32)
+        if s.ndim != 1 or s.shape[0] != q.shape[0]:
+            raise ValueError("scales must contain one value per weight row")
+        h = _vp()
+        with torch.cuda.device(q.device):
+            torch.cuda.current_stream(q.device).synchronize()   # the codes are complete before the legacy stream reads them
+            check(_lib.eb_compress_selected_codes_device(
+                ctypes.c_void_p(q.data_ptr()), _ptr(s, ctypes.c_float), q.shape[0], q.shape[1], int(selectedBits),
+                float(threshold), float(selectedError), _policy(decodePolicy), ctypes.byref(h)))
         return RuntimeMatrix(h)
 
     @staticmethod

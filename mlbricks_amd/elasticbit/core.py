@@ -102,8 +102,9 @@ def _moveBatch(batch: Any, device: torch.device) -> Any:
 
 
 @torch.inference_mode()
-def _selectBitsTorch(weight: torch.Tensor, calibration: np.ndarray, threshold: float
-                     ) -> tuple[int, float, np.ndarray | None, np.ndarray | None]:
+def _selectBitsTorch(weight: torch.Tensor, calibration: np.ndarray, threshold: float,
+                     codesOnDevice: bool = False
+                     ) -> tuple[int, float, np.ndarray | torch.Tensor | None, np.ndarray | None]:
     """Width selection on the model's GPU (core.py:112-195).
 
     For b = 3..15: s = max|w_r| / qmax (1 for a zero row), q = clamp(round(w/s)),
@@ -113,7 +114,9 @@ def _selectBitsTorch(weight: torch.Tensor, calibration: np.ndarray, threshold: f
     The errors of all thirteen widths come from one fused HIP pass over the
     weights (``width_errors_torch``); only the selected width is quantized
     here, and its codes and scales are returned so packing never
-    re-quantizes.
+    re-quantizes.  ``codesOnDevice`` keeps the codes as an int16 tensor on
+    the weight's device (for ``_compressSelectedCodesTorch``) instead of a
+    numpy copy.
     """
     if weight.device.type != "cuda":
         raise RuntimeError("ElasticBit GPU analyzer requires CUDA weights")
@@ -130,18 +133,21 @@ def _selectBitsTorch(weight: torch.Tensor, calibration: np.ndarray, threshold: f
         err = max(float(hw[bits - 3]), float(full[bits - 3]))
         if err <= float(threshold):
             codes, scales = _quantizeRowsTorch(w, bits)
+            if not codesOnDevice:
+                codes = np.ascontiguousarray(codes.cpu().numpy(), dtype=np.int16)
             return bits, err, codes, scales
     return 16, 0.0, None, None
 
 
-def _quantizeRowsTorch(weight: torch.Tensor, bits: int) -> tuple[np.ndarray, np.ndarray]:
-    """Codes and row scales of one width, as core.py:142-155 forms them."""
+def _quantizeRowsTorch(weight: torch.Tensor, bits: int) -> tuple[torch.Tensor, np.ndarray]:
+    """Codes (int16, on the weight's device) and row scales of one width, as
+    core.py:142-155 forms them."""
     w32 = weight.float()
     max_abs = w32.abs().amax(dim=1)
     qmax = float((1 << (bits - 1)) - 1)
     scale = torch.where(max_abs > 0.0, max_abs / qmax, torch.ones_like(max_abs))
     q = torch.round(w32 / scale[:, None]).clamp(min=-qmax, max=qmax)
-    codes = np.ascontiguousarray(q.to(torch.int16).cpu().numpy(), dtype=np.int16)
+    codes = q.to(torch.int16).contiguous()
     scales = np.ascontiguousarray(scale.float().cpu().numpy(), dtype=np.float32)
     return codes, scales
 
@@ -252,6 +258,17 @@ class RuntimeMatrix:
             raise ValueError("scales must contain one value per weight row")
         return cls(native.RuntimeMatrix._compressSelectedCodes(q, s, int(selectedBits), float(threshold),
                                                                float(selectedError), policy))
+
+    @classmethod
+    def _compressSelectedCodesTorch(cls, codes: torch.Tensor, scales: np.ndarray, selectedBits: int,
+                                    threshold: float, selectedError: float,
+                                    decodePolicy: str = "hardwareNative") -> "RuntimeMatrix":
+        """_compressSelectedCodes for codes that are an int16 tensor on the
+        HIP device: packed on the device, without a host copy of the codes."""
+        native = _requireNative()
+        policy = _checkPolicy(decodePolicy)
+        return cls(native.RuntimeMatrix._compressSelectedCodesTorch(codes, scales, int(selectedBits),
+                                                                    float(threshold), float(selectedError), policy))
 
     @classmethod
     def load(cls, path: str | Path, decodePolicy: str = "hardwareNative") -> "RuntimeMatrix":
@@ -645,14 +662,14 @@ class ElasticBit:
             if progress:
                 print(f"[ElasticBit] {index}/{len(work)} analyzing {names[0]} "
                       f"shape={tuple(module.weight.shape)} rows={calibration.shape[0]}", flush=True)
-            bits, err, codes, scales = _selectBitsTorch(module.weight, calibration, float(threshold))
-            torch.cuda.empty_cache()
+            bits, err, codes, scales = _selectBitsTorch(module.weight, calibration, float(threshold),
+                                                        codesOnDevice=True)
             if progress:
                 print(f"[ElasticBit] {index}/{len(work)} selected {bits}-bit error={err:.6g}", flush=True)
             with torch.cuda.device(device):
                 if bits <= 15:
-                    matrix = RuntimeMatrix._compressSelectedCodes(codes, scales, bits, float(threshold), err,
-                                                                  decodePolicy=policy)
+                    matrix = RuntimeMatrix._compressSelectedCodesTorch(codes, scales, bits, float(threshold), err,
+                                                                       decodePolicy=policy)
                 else:
                     weights = np.ascontiguousarray(module.weight.detach().cpu().float().numpy(), dtype=np.float32)
                     matrix = RuntimeMatrix._compressSelected(weights, bits, float(threshold), err,

@@ -210,6 +210,20 @@ def test_device_calls_fail_loudly_without_device():
         m._materializeTorch()
 
 
+def test_device_code_factory_validates_arguments():
+    lib = native.lib()
+    out = ctypes.c_void_p()
+    s = np.ones(4, np.float32)
+    sp = s.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+    assert lib.eb_compress_selected_codes_device(None, sp, 4, 32, 10, 0.01, 0.0, 0, ctypes.byref(out)) != 0
+    assert "null pointer" in lib.eb_last_error().decode()
+    p = ctypes.c_void_p(16)
+    assert lib.eb_compress_selected_codes_device(p, sp, 4, 32, 16, 0.01, 0.0, 0, ctypes.byref(out)) != 0
+    assert "3..15-bit" in lib.eb_last_error().decode()
+    assert lib.eb_compress_selected_codes_device(p, sp, 4, 32, 10, 0.01, 0.5, 0, ctypes.byref(out)) != 0
+    assert "does not satisfy threshold" in lib.eb_last_error().decode()
+
+
 def test_analyze_widths_validates_arguments():
     lib = native.lib()
     p = ctypes.c_void_p(16)

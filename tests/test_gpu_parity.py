@@ -353,6 +353,43 @@ def test_forward_multi_rejects_mismatched_inputs(native):
     assert "null pointer" in lib.eb_last_error().decode()
 
 
+@pytest.mark.parametrize("b", list(range(3, 16)))
+@pytest.mark.parametrize("rows,cols", [(7, 13), (33, 65), (5, 1000), (100, 2048), (1, 1)])
+def test_device_code_factory_matches_host_factory(native, b, rows, cols):
+    """Codes packed on the device (the compress path) give the same canonical
+    storage, byte for byte, as the host packer, and the same execution
+    layout; counts that are not multiples of 8 leave a partial last chunk."""
+    rng = np.random.default_rng(b * 13 + rows + cols)
+    q = _codes(rng, rows, cols, b)
+    s = rng.uniform(0.002, 0.05, size=rows).astype(np.float32)
+    host = native.RuntimeMatrix._compressSelectedCodes(q, s, b, 0.01, 0.0)
+    dev = native.RuntimeMatrix._compressSelectedCodesTorch(torch.from_numpy(q).cuda(), s, b, 0.01, 0.0)
+    hs, hp = host._canonical()
+    ds, dp = dev._canonical()
+    assert np.array_equal(hs, ds)
+    assert np.array_equal(hp, dp)
+    assert np.array_equal(dp, ora.pack_codes(q, b))
+    assert np.array_equal(dev._unpackCodesTorch().cpu().numpy(), q)
+    x = _x16(rng, 3, cols)
+    assert torch.equal(dev.forwardTorch(x), host.forwardTorch(x))
+
+
+def test_device_code_factory_rejects_bad_input(native):
+    rng = np.random.default_rng(2)
+    q = _codes(rng, 8, 64, 6)
+    s = np.ones(8, np.float32)
+    bad = torch.from_numpy(q).cuda()
+    bad[3, 17] = 32          # qmax is 31 at b = 6
+    with pytest.raises(ValueError, match="exceeds selected bit range"):
+        native.RuntimeMatrix._compressSelectedCodesTorch(bad, s, 6, 0.01, 0.0)
+    with pytest.raises(ValueError, match="one value per weight row"):
+        native.RuntimeMatrix._compressSelectedCodesTorch(torch.from_numpy(q).cuda(), s[:4], 6, 0.01, 0.0)
+    with pytest.raises(ValueError, match="int16 CUDA tensor"):
+        native.RuntimeMatrix._compressSelectedCodesTorch(torch.from_numpy(q), s, 6, 0.01, 0.0)
+    with pytest.raises(ValueError, match="3..15-bit"):
+        native.RuntimeMatrix._compressSelectedCodesTorch(torch.from_numpy(q).cuda(), s, 16, 0.01, 0.0)
+
+
 @pytest.mark.parametrize("M", [1, 24])
 def test_forward_unaligned_activation_pointer(native, M):
     rows, cols, b = 40, 256, 10
