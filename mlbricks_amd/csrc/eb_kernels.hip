@@ -594,11 +594,12 @@ __device__ __forceinline__ void decode_load_batch(const DevMatrix& m, Bits (&bit
 // Activation operands of one workgroup batch (steps base + wave*GPL + j):
 // from the LDS copy, or from global memory, zero past the last step.
 // Block mb holds activation rows 16 mb .. 16 mb + 15.
+// kshift: the column the LDS copy starts at (a chunk's first column, XL = 3).
 template <int GPL, int XL, int MB>
 __device__ __forceinline__ void decode_activations(half8 (&a)[MB][GPL][4], const DevMatrix& m, int base, int wave,
                                                    int quarter, const bool (&m_ok)[MB], int steps,
                                                    const uint16_t* const (&xrow)[MB],
-                                                   const uint16_t* const (&xsrow)[MB], int xvec) {
+                                                   const uint16_t* const (&xsrow)[MB], int xvec, int kshift = 0) {
     const int first = base + wave * GPL;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
@@ -609,7 +610,7 @@ __device__ __forceinline__ void decode_activations(half8 (&a)[MB][GPL][4], const
             if constexpr (XL != 0) {
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
-                    a[mb][j][t] = ok ? *reinterpret_cast<const half8*>(xsrow[mb] + k0 + 8 * t)
+                    a[mb][j][t] = ok ? *reinterpret_cast<const half8*>(xsrow[mb] + (k0 - kshift) + 8 * t)
                                      : half8{0, 0, 0, 0, 0, 0, 0, 0};
                 }
             } else if (ok) {
@@ -676,7 +677,12 @@ __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
     constexpr int kXDirect = (XL == 2 ? kXLdsDirectBytes : kXLdsBytes) / 16 / kThreads;
     static_assert(kXVecs >= 1, "LDS activation staging needs one uint4 per thread");
     static_assert(kThreads >= 256, "the epilogue stores the 16x16 tile with one thread per element");
-    extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   // [M][spr * 128], XL > 0 only
+    static_assert(XL != 3 || MB <= 2, "chunked staging holds at most 32 activation rows");
+    // XL = 3: K chunks of CT tiles, double-buffered; kBpc workgroup batches per chunk
+    constexpr int CT = MB == 1 ? 16 : 8;
+    constexpr int kBpc = CT / kBatch;
+    static_assert(XL != 3 || (kBpc >= 1 && CT % kBatch == 0), "a chunk holds whole workgroup batches");
+    extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   // XL = 1, 2: [M][spr * 128]; XL = 3: two chunks
 
     const int tile = select_matrix(mt, m, y, bias);
     const int lane = threadIdx.x & 63;
@@ -710,8 +716,31 @@ __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
     // aligned, so the staged copy is x itself and goes global -> LDS
     // directly, without registers; otherwise through registers, zero-padded.
     // XL = 2 is launched for xvec == 2 only.
-    const bool xdirect = XL == 2 || xvec == 2;
-    if constexpr (XL != 0) {
+    const bool xdirect = XL >= 2 || xvec == 2;
+    // XL = 3 (launched for xvec == 2): chunk c, columns c*CT*128 .. +CT*128,
+    // of Mp rows (M rounded up so that every wave issues Mp*CT/32 1 KB loads
+    // per chunk, which keeps the vector-memory counts uniform; padding rows
+    // repeat row M-1 and past the last column the source is clamped, neither
+    // is read) goes global -> LDS into buffer c % 2.
+    const int Mp = XL == 3 ? (M + 32 / CT - 1) / (32 / CT) * (32 / CT) : M;
+    const int chunk_halves = Mp * CT * kTileGroups * kGroup;
+    const int chunks = (steps + CT - 1) / CT;
+    auto stage_chunk = [&](int c) {
+        uint16_t* buf = xs + (c & 1) * chunk_halves;
+        const int per_wave = Mp * CT / 32;
+        for (int r = 0; r < per_wave; ++r) {
+            const int v = (r * WAVES + wave) * 64 + lane;          // 16-byte vector of the chunk
+            const int mi = v / (CT * 16);
+            const int j = v - mi * (CT * 16);
+            const int src_row = min(mi, M - 1);
+            const int src_col = min(c * CT * kTileGroups * kGroup + 8 * j, m.cols - 8);
+            __builtin_amdgcn_global_load_lds(x + static_cast<size_t>(src_row) * m.cols + src_col,
+                                             (lds_void_ptr)(buf + 8 * (v - lane)), 16, 0, 0);
+        }
+    };
+    if constexpr (XL == 3) {
+        stage_chunk(0);
+    } else if constexpr (XL != 0) {
         if (xdirect) {
 #pragma unroll
             for (int r = 0; r < kXDirect; ++r) {
@@ -762,7 +791,12 @@ __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
     // MI355X: one tile per wave plus the prefetch keeps ~40 KB per CU in
     // flight, which already covers the loaded HBM latency.
     decode_load_batch<GPL>(m, buf0, slot0, wave * GPL, steps);
-    if constexpr (XL != 0) {
+    if constexpr (XL == 3) {
+        // chunk 0 precedes the weight loads just issued
+        wait_vmcnt<GPL * GroupLoads<B, MODE>::value>();
+        barrier_after_wait();
+        if (chunks > 1) stage_chunk(1);
+    } else if constexpr (XL != 0) {
         if (xdirect) {
             // the activation loads precede the weight loads just issued
             wait_vmcnt<GPL * GroupLoads<B, MODE>::value>();
@@ -777,7 +811,26 @@ __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
         }
     }
     auto batch = [&](const Bits (&cur)[GPL], Bits (&nxt)[GPL], bool prefetch, int bi) {
-        decode_activations<GPL, XL, MB>(a, m, bi * kBatch, wave, quarter, m_ok, steps, xrow, xsrow, xvec);
+        int kshift = 0;
+        if constexpr (XL == 3) {
+            const int c = bi / kBpc;
+            if (bi > 0 && bi == c * kBpc) {
+                // First batch of chunk c: chunk c's loads are older than
+                // this batch's weights (issued during the previous batch),
+                // the only loads allowed to stay in flight.  The barrier
+                // also retires every wave's reads of chunk c - 1, whose
+                // buffer chunk c + 1 then refills.
+                wait_vmcnt<GPL * GroupLoads<B, MODE>::value>();
+                barrier_after_wait();
+                if (c + 1 < chunks) stage_chunk(c + 1);
+            }
+            kshift = c * CT * kTileGroups * kGroup;
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+                xsrow[mb] = xs + (c & 1) * chunk_halves + (m_ok[mb] ? 16 * mb + nl : 0) * (CT * kTileGroups * kGroup);
+            }
+        }
+        decode_activations<GPL, XL, MB>(a, m, bi * kBatch, wave, quarter, m_ok, steps, xrow, xsrow, xvec, kshift);
         if (prefetch) decode_load_batch<GPL>(m, nxt, slot0, (bi + 1) * kBatch + wave * GPL, steps);
         decode_mul_batch<B, MODE, GPL, MB>(cur, a, bi * kBatch + wave * GPL, steps, s, acc);
     };
@@ -2028,6 +2081,13 @@ void launch_narrow(const DevMatrix& m, const uint16_t* x, int64_t M, uint16_t* y
     }
 }
 
+// Activations too long to stage whole (x's rows whole tiles, M <= 32) go
+// through LDS in double-buffered K chunks (XL = 3) instead of per-lane L2
+// reads.
+#ifndef EBK_DECODE_CHUNKED
+#define EBK_DECODE_CHUNKED 1
+#endif
+
 // linear_decode_kernel for M <= 16 MB rows: activations staged in LDS when
 // they fit (directly up to kXLdsDirectBytes when x's rows are whole tiles),
 // read per lane from L2 otherwise.
@@ -2041,6 +2101,14 @@ void launch_decode(const DevMatrix& m, const uint16_t* x, int64_t M, uint16_t* y
     } else if (xvec == 2 && xbytes <= static_cast<size_t>(kXLdsDirectBytes)) {
         hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, 2, MB>), dim3(tiles),
                            dim3(64 * kDecodeWaves), xbytes, s, m, x, static_cast<int>(M), y, bias, xvec, mt);
+    } else if (MB <= 2 && xvec == 2 && EBK_DECODE_CHUNKED) {
+        if constexpr (MB <= 2) {
+            constexpr int CT = MB == 1 ? 16 : 8;     // as in the kernel
+            const int64_t Mp = (M + 32 / CT - 1) / (32 / CT) * (32 / CT);
+            const size_t lds = static_cast<size_t>(2 * Mp * CT * kTileGroups * kGroup * 2);
+            hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, 3, MB>), dim3(tiles),
+                               dim3(64 * kDecodeWaves), lds, s, m, x, static_cast<int>(M), y, bias, xvec, mt);
+        }
     } else {
         hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, 0, MB>), dim3(tiles),
                            dim3(64 * kDecodeWaves), 0, s, m, x, static_cast<int>(M), y, bias, xvec, mt);
