@@ -490,15 +490,16 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 // ---------------------------------------------------------------------------
-// decode kernel, M <= 16: one workgroup owns one row tile (16 weight rows);
+// decode kernel, M <= 64: one workgroup owns one row tile (16 weight rows);
 // its WAVES waves split the row tile's K tiles.  In step `st` lane l loads
 // slot l of tile (row tile, st) -- group 4*st + l/16 of row l%16 -- so a
 // wave's load is one contiguous block and one step feeds four
-// v_mfma_f32_16x16x32_f16 with 16 rows x 128 columns.  The K order inside a
-// group is the same for the A (activation) and B (weight) operands, so any
-// order is a valid dot product.
+// v_mfma_f32_16x16x32_f16 with 16 rows x 128 columns per block of 16
+// activation rows (MB blocks: each decoded operand feeds MB MFMAs).  The K
+// order inside a group is the same for the A (activation) and B (weight)
+// operands, so any order is a valid dot product.
 //
-// At M <= 16 the kernel is bound by HBM latency as much as by bandwidth: a
+// At small M the kernel is bound by HBM latency as much as by bandwidth: a
 // CU's share of a 4096 x 4096 b=10 matrix is ~80 KB, about what it must keep
 // in flight to cover the loaded DRAM latency.  Each wave therefore issues the
 // loads of GPL steps at once and, while it decodes and multiplies one batch,
@@ -510,8 +511,9 @@ __device__ __forceinline__ void wait_vmcnt() {
 // per workgroup in LDS.  XL = 1: up to kXLdsBytes, global -> LDS directly
 // when x's rows are whole tiles and 16-byte aligned, through registers
 // (zero-padded) otherwise.  XL = 2: up to kXLdsDirectBytes, direct only, so
-// no registers are held for it.  XL = 0: each lane with an activation row
-// loads its A operand from global memory per step.
+// no registers are held for it.  XL = 3: longer rows (whole tiles, M <= 32)
+// in double-buffered K chunks, direct.  XL = 0: each lane with an
+// activation row loads its A operand from global memory per step.
 // ---------------------------------------------------------------------------
 
 constexpr int kXLdsBytes = 32768;
@@ -2090,7 +2092,8 @@ void launch_narrow(const DevMatrix& m, const uint16_t* x, int64_t M, uint16_t* y
 
 // linear_decode_kernel for M <= 16 MB rows: activations staged in LDS when
 // they fit (directly up to kXLdsDirectBytes when x's rows are whole tiles),
-// read per lane from L2 otherwise.
+// in K chunks when they do not (whole tiles, M <= 32), read per lane from
+// L2 otherwise.
 template <int B, int MODE, int MB>
 void launch_decode(const DevMatrix& m, const uint16_t* x, int64_t M, uint16_t* y, const uint16_t* bias, int xvec,
                    hipStream_t s, const MultiTail& mt, int tiles) {
