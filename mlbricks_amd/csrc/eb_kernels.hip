@@ -1945,16 +1945,12 @@ struct MaterializeOp {
 #ifndef EBK_PREFILL_KS
 #define EBK_PREFILL_KS 2
 #endif
-#ifndef EBK_PREFILL_MI
-#define EBK_PREFILL_MI 4
-#endif
 #ifndef EBK_DECODE_WAVES
 #define EBK_DECODE_WAVES 8
 #endif
 #ifndef EBK_DECODE_GPL
 #define EBK_DECODE_GPL 1
 #endif
-constexpr int kPrefillMI = EBK_PREFILL_MI;
 constexpr int kPrefillKS = EBK_PREFILL_KS;
 constexpr int kDecodeWaves = EBK_DECODE_WAVES;
 constexpr int kDecodeGpl = EBK_DECODE_GPL;
