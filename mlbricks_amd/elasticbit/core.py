@@ -46,8 +46,11 @@ from .native_api import requireNative as _requireNative
 _VALID_POLICIES = {"hardwareNative", "fullPrecision"}
 _MODEL_FORMAT = "ElasticBitModel"
 _MODEL_FORMAT_VERSION = 1
-# Linear calls with at most this many activation rows qualify as "decode".
-_DECODE_MAX_ROWS = 16
+# Linear calls with at most this many activation rows qualify as "decode":
+# the native route runs its decode kernel up to 64 rows, where it reads the
+# weights once and leads the materialize + F.linear route by 3-4x, so a
+# batched decode is not tied to the route a long prompt chose.
+_DECODE_MAX_ROWS = 64
 
 
 def _checkPolicy(value: str) -> str:
