@@ -18,6 +18,10 @@ Every configuration beside the reference's execution format (markdown table):
 
     python bench.py --all-configs
 
+The forward over activation row counts 1..2048 on several shapes:
+
+    python bench.py --m-sweep
+
 Profiling helpers (same file, so the committed summaries name committed code):
 
     python bench.py --traffic-probe      # eager launches for rocprofv3 --pmc passes
@@ -69,6 +73,9 @@ def parse_args() -> argparse.Namespace:
                    help="run eager GEMV/prefill launches and a calibration copy for rocprofv3 --pmc")
     p.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
     p.add_argument("--summarize-trace", metavar="KERNEL_STATS_CSV")
+    p.add_argument("--m-sweep", action="store_true",
+                   help="time the forward over activation row counts 1..2048 on several shapes; "
+                        "prints a markdown table")
     p.add_argument("--all-configs", action="store_true",
                    help="time every BASELINE configuration (0-3) beside the reference's execution format; "
                         "prints a markdown table")
@@ -367,6 +374,45 @@ def all_configs(args) -> int:
     return 0
 
 
+def m_sweep(args) -> int:
+    """The forward over activation row counts on several shapes (b = 10,
+    synthetic codes), timed like the headline: every launch reads a weight
+    copy other than the last ones read (>= 512 MB of rotated copies, twice
+    the MALL), so no M is helped by a warm cache.  Shows where the launcher
+    moves between its kernels (GEMV, decode with 1/2/4 activation blocks,
+    prefill tiles)."""
+    import numpy as np
+    import torch
+
+    from mlbricks_amd.elasticbit import _native as native
+
+    shapes = ((4096, 4096), (11008, 4096), (4096, 11008), (14336, 4096), (1024, 1024), (1536, 384))
+    Ms = (1, 4, 16, 17, 32, 64, 96, 128, 256, 512, 1024, 2048)
+    lines = ["| N x K | " + " | ".join(f"M={M}" for M in Ms) + " |", "|---" * (len(Ms) + 1) + "|"]
+    for rows, cols in shapes:
+        rng = np.random.default_rng(rows + cols)
+        qm = 511
+        mats = []
+        per = None
+        while per is None or len(mats) * per < 2 * MALL_BYTES + per:
+            q = rng.integers(-qm, qm + 1, size=(rows, cols)).astype(np.int16)
+            s = rng.uniform(1e-4, 1e-3, size=rows).astype(np.float32)
+            mats.append(native.RuntimeMatrix._compressSelectedCodes(q, s, 10, 0.01, 0.0))
+            per = mats[0].executionBytes
+        cells = []
+        for M in Ms:
+            x = torch.randn(M, cols, generator=torch.Generator().manual_seed(1)).half().cuda()
+            ys = [torch.empty(M, rows, dtype=torch.float16, device="cuda") for _ in mats]
+            steps = 400 if M <= 64 else max(40, len(mats))
+            ms = time_graph([lambda m=m, y=y: m.forwardTorch(x, out=y) for m, y in zip(mats, ys)], steps, 3)
+            cells.append(f"{ms / steps * 1e3:.1f}")
+        lines.append(f"| {rows} x {cols} | " + " | ".join(cells) + " |")
+        log(lines[-1])
+        del mats
+    print("\n".join(lines), flush=True)
+    return 0
+
+
 def cpu_baseline(layer, seconds: float) -> dict:
     """The oracle's OpenMP GEMV (fp32 accumulate) over the same matrix and the
     same algorithmic bytes, on this host's cores (bounded to ~`seconds`)."""
@@ -561,6 +607,8 @@ def main() -> int:
         return traffic_probe(args)
     if args.all_configs:
         return all_configs(args)
+    if args.m_sweep:
+        return m_sweep(args)
 
     g = bench_gemv(args)
     ceiling = read_ceiling(g["bytes"], g["copies"], args.steps, args.warmup)
