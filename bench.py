@@ -22,6 +22,10 @@ The forward over activation row counts 1..2048 on several shapes:
 
     python bench.py --m-sweep
 
+configs[4]'s compressed Linears, one decode token at a time:
+
+    python bench.py --bolt-decode
+
 Profiling helpers (same file, so the committed summaries name committed code):
 
     python bench.py --traffic-probe      # eager launches for rocprofv3 --pmc passes
@@ -73,6 +77,9 @@ def parse_args() -> argparse.Namespace:
                    help="run eager GEMV/prefill launches and a calibration copy for rocprofv3 --pmc")
     p.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
     p.add_argument("--summarize-trace", metavar="KERNEL_STATS_CSV")
+    p.add_argument("--bolt-decode", action="store_true",
+                   help="configs[4]'s compressed Linears: one greedy decode token's 96 M = 1 forwards "
+                        "(12 layers) plus the tied fp16 LM head, timed per token")
     p.add_argument("--m-sweep", action="store_true",
                    help="time the forward over activation row counts 1..2048 on several shapes; "
                         "prints a markdown table")
@@ -374,6 +381,98 @@ def all_configs(args) -> int:
     return 0
 
 
+# configs[4]'s per-layer compressed Linears (out, in, bias), in block order:
+# avq.project, q/k/v/out_proj, head_gate (zero-initialised), fc, proj
+# (bolt/presets.py:93,155; bolt/enhanced_mqa.py:128-135; components.py:209-220).
+BOLT_LINEARS = (("avq.project", 2048, 1024, True), ("q_proj", 1024, 1024, False), ("k_proj", 64, 1024, False),
+                ("v_proj", 64, 1024, False), ("out_proj", 1024, 1024, False), ("head_gate", 16, 1024, True),
+                ("fc", 4096, 1024, False), ("proj", 1024, 4096, False))
+
+
+def bolt_decode(args) -> int:
+    """The compressed-Linear share of one configs[4] greedy decode token
+    (bolt/model.py:416-431): 12 layers x 8 ElasticBit Linears at M = 1, each
+    through the public module forward, plus the tied fp16 LM head
+    (32000 x 1024, F.linear).  The attention, retention and norm kernels
+    between them are not part of this build, so the tokens/s printed is a
+    ceiling set by the Linears alone.  Weights: nn.Linear's default init
+    under seed 0 (head_gate zero), compressed by ElasticBit.compress at
+    threshold 0.01 with 32 seeded N(0,1) calibration rows per Linear.  The
+    timed graph replays whole tokens back to back, as a decode loop does, so
+    whatever of the model fits in the MALL stays there as it would in a real
+    run."""
+    import torch
+    import torch.nn.functional as F
+
+    from mlbricks_amd import ElasticBit
+    from mlbricks_amd.elasticbit.core import RuntimeMatrix
+
+    torch.manual_seed(0)
+    layers = []
+    for li in range(12):
+        block = []
+        for name, out_f, in_f, bias in BOLT_LINEARS:
+            lin = torch.nn.Linear(in_f, out_f, bias=bias)
+            if name == "head_gate":
+                torch.nn.init.zeros_(lin.weight)
+            model = torch.nn.Sequential(lin).cuda().half().eval()
+            calib = torch.randn(32, in_f, generator=torch.Generator().manual_seed(2 + 100 * li + len(block))).half()
+            ElasticBit.compress(model, calib, 0.01)
+            block.append(model[0])
+        layers.append(block)
+    emb = (torch.randn(32000, 1024, generator=torch.Generator().manual_seed(0)) * 0.02).half().cuda()
+    xs = {w: torch.randn(1, w, generator=torch.Generator().manual_seed(1)).half().cuda() for w in (1024, 4096)}
+    widths = {}
+    nbytes = 0
+    for block in layers:
+        for (name, out_f, in_f, _), lin in zip(BOLT_LINEARS, block):
+            b = lin.matrix.storageBits
+            widths[b] = widths.get(b, 0) + 1
+            nbytes += algorithmic_bytes(out_f, in_f, b, 1)
+    head_bytes = 2 * 32000 * 1024 + 2 * 1024 + 2 * 32000
+    log(f"bolt decode: widths {dict(sorted(widths.items()))}, {nbytes / 1e6:.1f} MB of compressed Linears per token")
+
+    def token_separate():
+        for block in layers:
+            for (name, _, in_f, _), lin in zip(BOLT_LINEARS, block):
+                lin(xs[in_f])
+        F.linear(xs[1024], emb)
+
+    def token_fused():
+        # q, k, v and head_gate read the same activations: one multi-matrix
+        # launch per run of equal widths
+        for block in layers:
+            block[0](xs[1024])
+            group = [block[1], block[2], block[3], block[5]]
+            RuntimeMatrix.forwardTorchMulti([l.matrix for l in group], xs[1024], [l.bias for l in group])
+            block[4](xs[1024])
+            block[6](xs[1024])
+            block[7](xs[4096])
+        F.linear(xs[1024], emb)
+
+    def head_only():
+        F.linear(xs[1024], emb)
+
+    tokens = 20
+    rows = []
+    for label, fn in (("96 Linears + LM head", token_separate),
+                      ("q/k/v/head_gate fused + LM head", token_fused),
+                      ("LM head alone", head_only)):
+        us = time_graph([fn], tokens, 3) / tokens * 1e3
+        rows.append((label, us))
+        log(f"  {label}: {us:.1f} us per token")
+    head_us = rows[2][1]
+    lines = ["| per token | us | tokens/s ceiling | Linears' GB/s |", "|---|---|---|---|"]
+    for label, us in rows[:2]:
+        lin_us = us - head_us
+        lines.append(f"| {label} | {us:.1f} | {1e6 / us:.0f} | {nbytes / lin_us / 1e3:.0f} over {lin_us:.1f} us |")
+    lines.append(f"| {rows[2][0]} | {head_us:.1f} | - | {head_bytes / head_us / 1e3:.0f} (fp16 head) |")
+    print(f"configs[4] compressed Linears: widths {dict(sorted(widths.items()))}; "
+          f"{nbytes:,} B of compressed Linears + {head_bytes:,} B fp16 head per token", flush=True)
+    print("\n".join(lines), flush=True)
+    return 0
+
+
 def m_sweep(args) -> int:
     """The forward over activation row counts on several shapes (b = 10,
     synthetic codes), timed like the headline: every launch reads a weight
@@ -609,6 +708,8 @@ def main() -> int:
         return all_configs(args)
     if args.m_sweep:
         return m_sweep(args)
+    if args.bolt_decode:
+        return bolt_decode(args)
 
     g = bench_gemv(args)
     ceiling = read_ceiling(g["bytes"], g["copies"], args.steps, args.warmup)
