@@ -133,3 +133,41 @@ def test_grad_mode_with_requires_grad_takes_pytorch_route():
     y = model(x)
     y.float().sum().backward()
     assert x.grad is not None and x.grad.shape == x.shape
+
+
+def test_attention_projections_with_zero_head_gate_in_one_launch():
+    """A configs[4]-style attention block (bolt/enhanced_mqa.py:128-135):
+    q 1024x1024, k and v 64x1024 and a zero-initialised 16x1024 head_gate
+    with bias, each compressed by ElasticBit.compress.  The zero head_gate
+    selects b = 3 with scale 1 and all-zero codes, so its output is its bias
+    exactly.  RuntimeMatrix.forwardTorchMulti over the four equals each
+    matrix's own native forward bit for bit, and the modules' forwards
+    (whichever route the planner keeps) within the output tolerance."""
+    from mlbricks_amd import ElasticBit
+    from mlbricks_amd.elasticbit import RuntimeMatrix
+
+    torch.manual_seed(0)
+    layers = []
+    for out_f, bias, zero in ((1024, False, False), (64, False, False), (64, False, False), (16, True, True)):
+        lin = torch.nn.Linear(1024, out_f, bias=bias)
+        if zero:
+            torch.nn.init.zeros_(lin.weight)
+        model = torch.nn.Sequential(lin).cuda().half().eval()
+        ElasticBit.compress(model, torch.randn(32, 1024, generator=torch.Generator().manual_seed(out_f)).half(), 0.01)
+        layers.append(model[0])
+    gate = layers[3]
+    assert gate.matrix.storageBits == 3
+    scales, payload = gate.matrix._native._canonical()
+    assert np.all(scales == 1.0)
+    assert np.all(gate.matrix._native._unpackCodesTorch().cpu().numpy() == 0)
+    for M in (1, 4, 16):
+        x = torch.randn(M, 1024, generator=torch.Generator().manual_seed(M)).half().cuda()
+        with torch.inference_mode():
+            singles = [l.matrix._native.forwardTorch(x, bias=l.bias) for l in layers]
+            modules = [l(x) for l in layers]
+            fused = RuntimeMatrix.forwardTorchMulti([l.matrix for l in layers], x, [l.bias for l in layers])
+        for j, (a, b, c) in enumerate(zip(fused, singles, modules)):
+            assert torch.equal(a, b), (M, j)
+            ref = float(c.float().abs().max())
+            assert float((a.float() - c.float()).abs().max()) <= 2e-3 * max(ref, 1e-6), (M, j)
+        assert torch.equal(fused[3], gate.bias.detach().expand(M, 16))
