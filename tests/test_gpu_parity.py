@@ -651,3 +651,28 @@ def _check_prefill_shape(native, rows, cols, M, b, policy):
     payload = ora.pack_codes(q[:sub_r], b)
     ref = _reference(payload, s[:sub_r], sub_r, cols, b, x[-sub_m:].cpu().numpy().view(np.uint16), policy)
     assert _rel_max(y[-sub_m:, :sub_r].float().cpu().numpy(), ref) <= TOL
+
+
+def test_forward_leading_dims_and_empty_inputs(native):
+    """The forward takes x of shape [..., cols] (configs[0] feeds [2, 128,
+    384]) and returns [..., rows]: a 3-D input equals its 2-D flattening bit
+    for bit, and inputs with no rows ([0, cols], [2, 0, cols]) return empty
+    outputs of the right shape without a launch, through forwardTorch and
+    forward_torch_multi alike."""
+    rng = np.random.default_rng(77)
+    rows, cols, b = 96, 384, 8
+    q = _codes(rng, rows, cols, b)
+    s = rng.uniform(0.002, 0.05, size=rows).astype(np.float32)
+    m = native.RuntimeMatrix._compressSelectedCodes(q, s, b, 0.01, 0.0)
+    for lead in ((2, 128), (3, 5), (1, 1), (4, 1, 2)):
+        x = _x16(rng, int(np.prod(lead)), cols).view(*lead, cols)
+        y = m.forwardTorch(x)
+        assert y.shape == (*lead, rows)
+        assert torch.equal(y.reshape(-1, rows), m.forwardTorch(x.reshape(-1, cols)))
+        ym = native.forward_torch_multi([m, m], x)
+        assert all(torch.equal(t, y) for t in ym)
+    for shape in ((0, cols), (2, 0, cols)):
+        x = torch.empty(shape, dtype=torch.float16, device="cuda")
+        y = m.forwardTorch(x)
+        assert y.shape == (*shape[:-1], rows)
+        assert [t.shape for t in native.forward_torch_multi([m], x)] == [(*shape[:-1], rows)]
