@@ -676,3 +676,29 @@ def test_forward_leading_dims_and_empty_inputs(native):
         y = m.forwardTorch(x)
         assert y.shape == (*shape[:-1], rows)
         assert [t.shape for t in native.forward_torch_multi([m], x)] == [(*shape[:-1], rows)]
+
+
+def test_activations_beyond_4_gib_use_64_bit_addressing(native):
+    """An activation matrix larger than 4 GiB (66000 x 32768 fp16, 4.33 GB):
+    the prefill tiles address x with 32-bit byte offsets, so the launcher
+    hands this input to linear_gemm_kernel, whose addressing is 64-bit.  The
+    rows on both sides of the 4 GiB boundary (row 65536 starts at byte
+    2^32), the first rows and the last rows match the fp64 oracle."""
+    rows, cols, M, b = 32, 32768, 66000, 10
+    rng = np.random.default_rng(4096)
+    q = _codes(rng, rows, cols, b)
+    s = rng.uniform(0.002, 0.05, size=rows).astype(np.float32)
+    m = native.RuntimeMatrix._compressSelectedCodes(q, s, b, 0.01, 0.0)
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn(M, cols, generator=gen, device="cuda", dtype=torch.float16)
+    assert x.numel() * 2 > (1 << 32)
+    y = m.forwardTorch(x)
+    torch.cuda.synchronize()
+    idx = np.array([0, 1, 2, 65533, 65534, 65535, 65536, 65537, 65538, M - 3, M - 2, M - 1])
+    sel = torch.from_numpy(idx).cuda()
+    xs = x.index_select(0, sel).cpu().numpy().view(np.uint16)
+    got = y.index_select(0, sel).float().cpu().numpy()
+    del x, y
+    torch.cuda.empty_cache()
+    ref = _reference(ora.pack_codes(q, b), s, rows, cols, b, xs)
+    assert _rel_max(got, ref) <= TOL
