@@ -2035,15 +2035,22 @@ inline int narrow_workgroups(int64_t M, int rows, int mi, int cus) {
 // row tile re-reads all M x K activations from L2; the 64-row prefill tiles
 // are few at these M, so their time is one tile's walk over K per round.
 // Fitted on MI355X at b = 10 (us): decode ~ max(weight bytes at 5 TB/s,
-// rtiles * M * K * 2 at 6.5 TB/s) + 2; prefill ~ (3 + 0.005 K) per round
-// (4096 x 4096 M = 64: decode 19.8 against prefill ~24; 11008 x 4096
-// M = 32: decode 30.2 against prefill ~25).
+// rtiles * M * K * 2 at R) + 2, with R the rate of the activation path the
+// decode launch takes (6.5 TB/s staged whole up to 32 KB, 5.2 TB/s staged
+// in LDS beyond that, 7.5 TB/s read per lane from L2); prefill ~
+// (3 + 0.005 K) per round.  Measured (decode against prefill, us):
+// 4096 x 4096 M = 64 19.8 / 24.6; 11008 x 4096 M = 17 20.5 / 23.3,
+// M = 24 25.6 / 23.7; 14336 x 4096 M = 17 26.1 / 24.5; 4096 x 11008
+// M = 64 46.8 / 61.1.
 inline bool prefer_decode(int64_t M, const DevMatrix& m, int cus) {
     if (M <= 16) return true;
     if (M > kDecodeMaxM) return false;
     const double wbytes = static_cast<double>(m.rows) * m.cols * (m.bits == 16 ? 16 : m.bits) / 8.0;
     const double xbytes = static_cast<double>(m.rtiles) * static_cast<double>(M) * m.cols * 2.0;
-    const double t_decode = std::max(wbytes / 5.0e6, xbytes / 6.5e6) + 2.0;
+    const double staged = static_cast<double>(M) * m.spr * kTileGroups * kGroup * 2.0;   // as launch_decode
+    const double rate = staged <= kXLdsBytes ? 6.5e6
+                        : (staged <= kXLdsDirectBytes || M <= 32) ? 5.2e6 : 7.5e6;
+    const double t_decode = std::max(wbytes / 5.0e6, xbytes / rate) + 2.0;
     const int wgs = narrow_workgroups(M, m.rows, 2, cus);
     const double rounds = static_cast<double>((wgs + cus - 1) / cus);
     const double t_prefill = (3.0 + 0.005 * m.cols) * rounds;
