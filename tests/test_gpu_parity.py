@@ -702,3 +702,49 @@ def test_activations_beyond_4_gib_use_64_bit_addressing(native):
     torch.cuda.empty_cache()
     ref = _reference(ora.pack_codes(q, b), s, rows, cols, b, xs)
     assert _rel_max(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("M", [8, 16, 17])
+@pytest.mark.parametrize("rows", [11000, 14336])
+def test_decode_workgroups_loop_over_row_tiles(native, rows, M):
+    """With x staged whole in LDS beyond 32 KB (M x 4096 here), the decode
+    launch holds only the workgroups that fit on the chip at once and each
+    loops over row tiles, staging x once.  With 688 or 896 row tiles (the
+    last one partial at 11000 rows) every workgroup takes several.  All rows
+    match the fp32 product of the decoded weights, and the first and last 24
+    rows the fp64 oracle."""
+    cols, b = 4096, 10
+    rng = np.random.default_rng(rows + M)
+    q = _codes(rng, rows, cols, b)
+    s = rng.uniform(0.002, 0.05, size=rows).astype(np.float32)
+    m = native.RuntimeMatrix._compressSelectedCodes(q, s, b, 0.01, 0.0)
+    x = _x16(rng, M, cols)
+    y = m.forwardTorch(x)
+    wd = m._materializeTorch().float()
+    full = torch.matmul(x.float(), wd.T.contiguous())
+    err = float((y.float() - full).abs().max() / full.abs().max())
+    assert err <= TOL, err
+    xs = x.cpu().numpy().view(np.uint16)
+    for sl in (slice(0, 24), slice(rows - 24, rows)):
+        ref = _reference(ora.pack_codes(q[sl], b), s[sl], 24, cols, b, xs)
+        assert _rel_max(y[:, sl].float().cpu().numpy(), ref) <= TOL
+
+
+@pytest.mark.parametrize("M", [16, 17])
+def test_multi_matrix_decode_loops_over_tiles_of_every_matrix(native, M):
+    """A multi-matrix decode launch (Gate/Up: two 11008 x 4096 matrices and a
+    third of another width) whose workgroups loop over row tiles crossing
+    from one matrix to the next returns each matrix's own forward bit for
+    bit."""
+    cols = 4096
+    rng = np.random.default_rng(900 + M)
+    mats = []
+    for rows, b in ((11008, 10), (11008, 10), (4096, 10)):
+        q = _codes(rng, rows, cols, b)
+        s = rng.uniform(0.002, 0.05, size=rows).astype(np.float32)
+        mats.append(native.RuntimeMatrix._compressSelectedCodes(q, s, b, 0.01, 0.0))
+    x = _x16(rng, M, cols)
+    biases = [torch.from_numpy(rng.standard_normal(mm.rows).astype(np.float16)).cuda() for mm in mats]
+    ys = native.forward_torch_multi(mats, x, biases)
+    for j, (mm, yj) in enumerate(zip(mats, ys)):
+        assert torch.equal(yj, mm.forwardTorch(x, bias=biases[j])), j
