@@ -517,10 +517,6 @@ __device__ __forceinline__ void wait_vmcnt() {
 // ---------------------------------------------------------------------------
 
 constexpr int kXLdsBytes = 32768;
-constexpr size_t kLdsPerCu = 163840;       // gfx950: 160 KB of LDS per CU
-#ifndef EBK_DECODE_PERSIST
-#define EBK_DECODE_PERSIST 1
-#endif
 constexpr int kXLdsDirectBytes = 147456;   // 16 rows of 4608 halves
 
 // One group's weight bits as held in registers between load and decode.
@@ -654,7 +650,8 @@ __device__ __forceinline__ void decode_mul_batch(const Bits (&cur)[GPL], const h
 // The matrix, row tile, output and bias of this workgroup in a launch over
 // several matrices (MultiTail); a single-matrix launch keeps its arguments.
 __device__ __forceinline__ int select_matrix(const MultiTail& mt, DevMatrix& m, uint16_t* __restrict__& y,
-                                             const uint16_t* __restrict__& bias, int tile) {
+                                             const uint16_t* __restrict__& bias) {
+    int tile = blockIdx.x;
     if (mt.count > 1) {
         int base = 0;
 #pragma unroll
@@ -673,8 +670,8 @@ __device__ __forceinline__ int select_matrix(const MultiTail& mt, DevMatrix& m, 
 
 template <int B, int MODE, int WAVES, int GPL, int XL, int MB>
 __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
-    const DevMatrix m0, const uint16_t* __restrict__ x, int M, uint16_t* __restrict__ y0,
-    const uint16_t* __restrict__ bias0, int xvec, const MultiTail mt, int ntiles) {
+    DevMatrix m, const uint16_t* __restrict__ x, int M, uint16_t* __restrict__ y,
+    const uint16_t* __restrict__ bias, int xvec, const MultiTail mt) {
     using Bits = GroupBits<B, MODE>;
     constexpr int kThreads = 64 * WAVES;
     constexpr int kBatch = WAVES * GPL;              // steps per workgroup batch
@@ -689,204 +686,188 @@ __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
     static_assert(XL != 3 || (kBpc >= 1 && CT % kBatch == 0), "a chunk holds whole workgroup batches");
     extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   // XL = 1, 2: [M][spr * 128]; XL = 3: two chunks
 
-    // XL = 2 launches at most as many workgroups as fit on the chip at once
-    // (x staged whole holds up to 144 KB of LDS): each takes row tiles
-    // blockIdx.x, blockIdx.x + gridDim.x, ... (of any matrix of a launch
-    // over several) and stages x for the first only.  Every other launch
-    // has one workgroup per row tile.
-    for (int tile_i = blockIdx.x, it = 0; tile_i < ntiles; tile_i += gridDim.x, ++it) {
-        DevMatrix m = m0;
-        uint16_t* __restrict__ y = y0;
-        const uint16_t* __restrict__ bias = bias0;
-        const int tile = select_matrix(mt, m, y, bias, tile_i);
-        const int lane = threadIdx.x & 63;
-        const int wave = threadIdx.x >> 6;
-        const int nl = lane & 15;
-        const int quarter = lane >> 4;
-        const int row = tile * kTileRows + nl;
-        bool m_ok[MB];                                   // activation row 16 mb + nl of the A operand
+    const int tile = select_matrix(mt, m, y, bias);
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int nl = lane & 15;
+    const int quarter = lane >> 4;
+    const int row = tile * kTileRows + nl;
+    bool m_ok[MB];                                   // activation row 16 mb + nl of the A operand
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb) m_ok[mb] = 16 * mb + nl < M;
-        const int steps = m.spr;
-        const int kpad = steps * kTileGroups * kGroup;
-        float s = 0.0f;
-        if constexpr (MODE == kModeW) s = row < m.rows ? m.scales[row] : 0.0f;
-        // Thread o < 256 stores output (4*(o%64/16) + o/64, n0 + o%16) at the end;
-        // its row scale and bias are loaded now, ahead of the weights, so that
-        // the epilogue does not wait for another memory round trip.
-        const int on = tile * kTileRows + (threadIdx.x & 15);
-        float out_scale = 1.0f;
-        uint16_t out_bias = 0;
-        if (threadIdx.x < 256 && on < m.rows) {
-            if constexpr (MODE == kModeQ) out_scale = m.scales[on];
-            if (bias) out_bias = bias[on];
-        }
-        // Slot of this lane in the row tile's first tile; step st adds st * 64.
-        const size_t slot0 = static_cast<size_t>(tile) * steps * kTileSlots + lane;
+    for (int mb = 0; mb < MB; ++mb) m_ok[mb] = 16 * mb + nl < M;
+    const int steps = m.spr;
+    const int kpad = steps * kTileGroups * kGroup;
+    float s = 0.0f;
+    if constexpr (MODE == kModeW) s = row < m.rows ? m.scales[row] : 0.0f;
+    // Thread o < 256 stores output (4*(o%64/16) + o/64, n0 + o%16) at the end;
+    // its row scale and bias are loaded now, ahead of the weights, so that
+    // the epilogue does not wait for another memory round trip.
+    const int on = tile * kTileRows + (threadIdx.x & 15);
+    float out_scale = 1.0f;
+    uint16_t out_bias = 0;
+    if (threadIdx.x < 256 && on < m.rows) {
+        if constexpr (MODE == kModeQ) out_scale = m.scales[on];
+        if (bias) out_bias = bias[on];
+    }
+    // Slot of this lane in the row tile's first tile; step st adds st * 64.
+    const size_t slot0 = static_cast<size_t>(tile) * steps * kTileSlots + lane;
 
-        uint4 xv[XL == 1 ? kXVecs : 1];
-        const int vpr = kpad / 8;                        // uint4 vectors per staged row
-        // xvec == 2: rows are whole tiles wide (cols == kpad) and x is 16-byte
-        // aligned, so the staged copy is x itself and goes global -> LDS
-        // directly, without registers; otherwise through registers, zero-padded.
-        // XL = 2 is launched for xvec == 2 only.
-        const bool xdirect = XL >= 2 || xvec == 2;
-        // XL = 3 (launched for xvec == 2): chunk c, columns c*CT*128 .. +CT*128,
-        // of Mp rows (M rounded up so that every wave issues Mp*CT/32 1 KB loads
-        // per chunk, which keeps the vector-memory counts uniform; padding rows
-        // repeat row M-1 and past the last column the source is clamped, neither
-        // is read) goes global -> LDS into buffer c % 2.
-        const int Mp = XL == 3 ? (M + 32 / CT - 1) / (32 / CT) * (32 / CT) : M;
-        const int chunk_halves = Mp * CT * kTileGroups * kGroup;
-        const int chunks = (steps + CT - 1) / CT;
-        auto stage_chunk = [&](int c) {
-            uint16_t* buf = xs + (c & 1) * chunk_halves;
-            const int per_wave = Mp * CT / 32;
-            for (int r = 0; r < per_wave; ++r) {
-                const int v = (r * WAVES + wave) * 64 + lane;          // 16-byte vector of the chunk
-                const int mi = v / (CT * 16);
-                const int j = v - mi * (CT * 16);
-                const int src_row = min(mi, M - 1);
-                const int src_col = min(c * CT * kTileGroups * kGroup + 8 * j, m.cols - 8);
-                __builtin_amdgcn_global_load_lds(x + static_cast<size_t>(src_row) * m.cols + src_col,
-                                                 (lds_void_ptr)(buf + 8 * (v - lane)), 16, 0, 0);
-            }
-        };
-        if constexpr (XL == 3) {
-            stage_chunk(0);
-        } else if constexpr (XL != 0) {
-            if (it > 0) {
-                // staged for the first tile
-            } else if (xdirect) {
+    uint4 xv[XL == 1 ? kXVecs : 1];
+    const int vpr = kpad / 8;                        // uint4 vectors per staged row
+    // xvec == 2: rows are whole tiles wide (cols == kpad) and x is 16-byte
+    // aligned, so the staged copy is x itself and goes global -> LDS
+    // directly, without registers; otherwise through registers, zero-padded.
+    // XL = 2 is launched for xvec == 2 only.
+    const bool xdirect = XL >= 2 || xvec == 2;
+    // XL = 3 (launched for xvec == 2): chunk c, columns c*CT*128 .. +CT*128,
+    // of Mp rows (M rounded up so that every wave issues Mp*CT/32 1 KB loads
+    // per chunk, which keeps the vector-memory counts uniform; padding rows
+    // repeat row M-1 and past the last column the source is clamped, neither
+    // is read) goes global -> LDS into buffer c % 2.
+    const int Mp = XL == 3 ? (M + 32 / CT - 1) / (32 / CT) * (32 / CT) : M;
+    const int chunk_halves = Mp * CT * kTileGroups * kGroup;
+    const int chunks = (steps + CT - 1) / CT;
+    auto stage_chunk = [&](int c) {
+        uint16_t* buf = xs + (c & 1) * chunk_halves;
+        const int per_wave = Mp * CT / 32;
+        for (int r = 0; r < per_wave; ++r) {
+            const int v = (r * WAVES + wave) * 64 + lane;          // 16-byte vector of the chunk
+            const int mi = v / (CT * 16);
+            const int j = v - mi * (CT * 16);
+            const int src_row = min(mi, M - 1);
+            const int src_col = min(c * CT * kTileGroups * kGroup + 8 * j, m.cols - 8);
+            __builtin_amdgcn_global_load_lds(x + static_cast<size_t>(src_row) * m.cols + src_col,
+                                             (lds_void_ptr)(buf + 8 * (v - lane)), 16, 0, 0);
+        }
+    };
+    if constexpr (XL == 3) {
+        stage_chunk(0);
+    } else if constexpr (XL != 0) {
+        if (xdirect) {
 #pragma unroll
-                for (int r = 0; r < kXDirect; ++r) {
-                    const int i = threadIdx.x + r * kThreads;
-                    if (i < M * vpr) {
-                        __builtin_amdgcn_global_load_lds(x + 8 * i,
-                                                         (lds_void_ptr)(xs + 8 * (r * kThreads + (threadIdx.x & ~63))),
-                                                         16, 0, 0);
-                    }
+            for (int r = 0; r < kXDirect; ++r) {
+                const int i = threadIdx.x + r * kThreads;
+                if (i < M * vpr) {
+                    __builtin_amdgcn_global_load_lds(x + 8 * i,
+                                                     (lds_void_ptr)(xs + 8 * (r * kThreads + (threadIdx.x & ~63))),
+                                                     16, 0, 0);
                 }
-            } else if constexpr (XL == 1) {
+            }
+        } else if constexpr (XL == 1) {
 #pragma unroll
-                for (int r = 0; r < kXVecs; ++r) {
-                    const int i = threadIdx.x + r * kThreads;
-                    xv[r] = make_uint4(0, 0, 0, 0);
-                    if (i < M * vpr) {
-                        const int mi = i / vpr;
-                        xv[r] = load_x8(x, mi, (i - mi * vpr) * 8, m.cols, xvec != 0);
-                    }
+            for (int r = 0; r < kXVecs; ++r) {
+                const int i = threadIdx.x + r * kThreads;
+                xv[r] = make_uint4(0, 0, 0, 0);
+                if (i < M * vpr) {
+                    const int mi = i / vpr;
+                    xv[r] = load_x8(x, mi, (i - mi * vpr) * 8, m.cols, xvec != 0);
                 }
             }
         }
+    }
 
-        // Steps past the end (steps % kBatch != 0) reload the last tile; they
-        // meet zero activations, and raw fp16 weights, which could hold Inf or
-        // NaN, are zeroed there.
-        floatx4 acc[MB];
+    // Steps past the end (steps % kBatch != 0) reload the last tile; they
+    // meet zero activations, and raw fp16 weights, which could hold Inf or
+    // NaN, are zeroed there.
+    floatx4 acc[MB];
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb) acc[mb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-        Bits buf0[GPL], buf1[GPL];
-        const int nb = (steps + kBatch - 1) / kBatch;    // workgroup batches
-        const uint16_t* xrow[MB];
-        const uint16_t* xsrow[MB];
+    for (int mb = 0; mb < MB; ++mb) acc[mb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    Bits buf0[GPL], buf1[GPL];
+    const int nb = (steps + kBatch - 1) / kBatch;    // workgroup batches
+    const uint16_t* xrow[MB];
+    const uint16_t* xsrow[MB];
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-            const int r = m_ok[mb] ? 16 * mb + nl : 0;
-            xrow[mb] = x + static_cast<size_t>(r) * m.cols;
-            xsrow[mb] = xs + static_cast<size_t>(r) * kpad;
-        }
-        half8 a[MB][GPL][4];
+    for (int mb = 0; mb < MB; ++mb) {
+        const int r = m_ok[mb] ? 16 * mb + nl : 0;
+        xrow[mb] = x + static_cast<size_t>(r) * m.cols;
+        xsrow[mb] = xs + static_cast<size_t>(r) * kpad;
+    }
+    half8 a[MB][GPL][4];
 
-        // One batch is prefetched while the previous one is multiplied (two
-        // register buffers alternate, so no register copy waits on loads in
-        // flight; every branch is uniform).  The activations of a batch are read
-        // before the next batch's weights are issued, so that waiting for them
-        // (global loads when they are not staged in LDS) does not wait for those
-        // weights.  Keeping more batches in flight per wave measured slower on
-        // MI355X: one tile per wave plus the prefetch keeps ~40 KB per CU in
-        // flight, which already covers the loaded HBM latency.
-        decode_load_batch<GPL>(m, buf0, slot0, wave * GPL, steps);
-        if constexpr (XL == 3) {
-            // chunk 0 precedes the weight loads just issued
+    // One batch is prefetched while the previous one is multiplied (two
+    // register buffers alternate, so no register copy waits on loads in
+    // flight; every branch is uniform).  The activations of a batch are read
+    // before the next batch's weights are issued, so that waiting for them
+    // (global loads when they are not staged in LDS) does not wait for those
+    // weights.  Keeping more batches in flight per wave measured slower on
+    // MI355X: one tile per wave plus the prefetch keeps ~40 KB per CU in
+    // flight, which already covers the loaded HBM latency.
+    decode_load_batch<GPL>(m, buf0, slot0, wave * GPL, steps);
+    if constexpr (XL == 3) {
+        // chunk 0 precedes the weight loads just issued
+        wait_vmcnt<GPL * GroupLoads<B, MODE>::value>();
+        barrier_after_wait();
+        if (chunks > 1) stage_chunk(1);
+    } else if constexpr (XL != 0) {
+        if (xdirect) {
+            // the activation loads precede the weight loads just issued
             wait_vmcnt<GPL * GroupLoads<B, MODE>::value>();
             barrier_after_wait();
-            if (chunks > 1) stage_chunk(1);
-        } else if constexpr (XL != 0) {
-            if (it > 0) {
-                // staged for the first tile
-            } else if (xdirect) {
-                // the activation loads precede the weight loads just issued
+        } else if constexpr (XL == 1) {
+#pragma unroll
+            for (int r = 0; r < kXVecs; ++r) {
+                const int i = threadIdx.x + r * kThreads;
+                if (i < M * vpr) *reinterpret_cast<uint4*>(xs + 8 * i) = xv[r];
+            }
+            __syncthreads();
+        }
+    }
+    auto batch = [&](const Bits (&cur)[GPL], Bits (&nxt)[GPL], bool prefetch, int bi) {
+        int kshift = 0;
+        if constexpr (XL == 3) {
+            const int c = bi / kBpc;
+            if (bi > 0 && bi == c * kBpc) {
+                // First batch of chunk c: chunk c's loads are older than
+                // this batch's weights (issued during the previous batch),
+                // the only loads allowed to stay in flight.  The barrier
+                // also retires every wave's reads of chunk c - 1, whose
+                // buffer chunk c + 1 then refills.
                 wait_vmcnt<GPL * GroupLoads<B, MODE>::value>();
                 barrier_after_wait();
-            } else if constexpr (XL == 1) {
+                if (c + 1 < chunks) stage_chunk(c + 1);
+            }
+            kshift = c * CT * kTileGroups * kGroup;
 #pragma unroll
-                for (int r = 0; r < kXVecs; ++r) {
-                    const int i = threadIdx.x + r * kThreads;
-                    if (i < M * vpr) *reinterpret_cast<uint4*>(xs + 8 * i) = xv[r];
-                }
-                __syncthreads();
+            for (int mb = 0; mb < MB; ++mb) {
+                xsrow[mb] = xs + (c & 1) * chunk_halves + (m_ok[mb] ? 16 * mb + nl : 0) * (CT * kTileGroups * kGroup);
             }
         }
-        auto batch = [&](const Bits (&cur)[GPL], Bits (&nxt)[GPL], bool prefetch, int bi) {
-            int kshift = 0;
-            if constexpr (XL == 3) {
-                const int c = bi / kBpc;
-                if (bi > 0 && bi == c * kBpc) {
-                    // First batch of chunk c: chunk c's loads are older than
-                    // this batch's weights (issued during the previous batch),
-                    // the only loads allowed to stay in flight.  The barrier
-                    // also retires every wave's reads of chunk c - 1, whose
-                    // buffer chunk c + 1 then refills.
-                    wait_vmcnt<GPL * GroupLoads<B, MODE>::value>();
-                    barrier_after_wait();
-                    if (c + 1 < chunks) stage_chunk(c + 1);
-                }
-                kshift = c * CT * kTileGroups * kGroup;
-#pragma unroll
-                for (int mb = 0; mb < MB; ++mb) {
-                    xsrow[mb] = xs + (c & 1) * chunk_halves + (m_ok[mb] ? 16 * mb + nl : 0) * (CT * kTileGroups * kGroup);
-                }
-            }
-            decode_activations<GPL, XL, MB>(a, m, bi * kBatch, wave, quarter, m_ok, steps, xrow, xsrow, xvec, kshift);
-            if (prefetch) decode_load_batch<GPL>(m, nxt, slot0, (bi + 1) * kBatch + wave * GPL, steps);
-            decode_mul_batch<B, MODE, GPL, MB>(cur, a, bi * kBatch + wave * GPL, steps, s, acc);
-        };
-        for (int bi = 0;; bi += 2) {
-            if (bi + 1 >= nb) {
-                batch(buf0, buf1, false, bi);
-                break;
-            }
-            batch(buf0, buf1, true, bi);
-            if (bi + 2 >= nb) {
-                batch(buf1, buf0, false, bi + 1);
-                break;
-            }
-            batch(buf1, buf0, true, bi + 1);
+        decode_activations<GPL, XL, MB>(a, m, bi * kBatch, wave, quarter, m_ok, steps, xrow, xsrow, xvec, kshift);
+        if (prefetch) decode_load_batch<GPL>(m, nxt, slot0, (bi + 1) * kBatch + wave * GPL, steps);
+        decode_mul_batch<B, MODE, GPL, MB>(cur, a, bi * kBatch + wave * GPL, steps, s, acc);
+    };
+    for (int bi = 0;; bi += 2) {
+        if (bi + 1 >= nb) {
+            batch(buf0, buf1, false, bi);
+            break;
         }
+        batch(buf0, buf1, true, bi);
+        if (bi + 2 >= nb) {
+            batch(buf1, buf0, false, bi + 1);
+            break;
+        }
+        batch(buf1, buf0, true, bi + 1);
+    }
 
-        // cross-wave reduction of each 16x16 fp32 block, one block at a time
-        __shared__ floatx4 red[WAVES][64];
+    // cross-wave reduction of each 16x16 fp32 block, one block at a time
+    __shared__ floatx4 red[WAVES][64];
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-            if (mb > 0) __syncthreads();
-            red[wave][lane] = acc[mb];
-            __syncthreads();
-            if (threadIdx.x < 256) {
-                const int src = threadIdx.x & 63;
-                const int e = threadIdx.x >> 6;
-                float v = 0.0f;
+    for (int mb = 0; mb < MB; ++mb) {
+        if (mb > 0) __syncthreads();
+        red[wave][lane] = acc[mb];
+        __syncthreads();
+        if (threadIdx.x < 256) {
+            const int src = threadIdx.x & 63;
+            const int e = threadIdx.x >> 6;
+            float v = 0.0f;
 #pragma unroll
-                for (int w = 0; w < WAVES; ++w) v += red[w][src][e];
-                const int mi = 16 * mb + 4 * (src >> 4) + e;   // D[4*(l/16)+e][l%16] of block mb
-                if (mi < M && on < m.rows) {
-                    y[static_cast<size_t>(mi) * m.rows + on] =
-                        epilogue<MODE>(v, out_scale, bias != nullptr, out_bias);
-                }
+            for (int w = 0; w < WAVES; ++w) v += red[w][src][e];
+            const int mi = 16 * mb + 4 * (src >> 4) + e;   // D[4*(l/16)+e][l%16] of block mb
+            if (mi < M && on < m.rows) {
+                y[static_cast<size_t>(mi) * m.rows + on] =
+                    epilogue<MODE>(v, out_scale, bias != nullptr, out_bias);
             }
         }
-        // the next tile's epilogue rewrites red[]
-        if (tile_i + static_cast<int>(gridDim.x) < ntiles) __syncthreads();
     }
 }
 
@@ -917,7 +898,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void linear_gemv_kernel(
     extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   // [cols], cols % 128 == 0
     __shared__ float red[kGemvWaves][kTileRows];
 
-    const int tile = select_matrix(mt, m, y, bias, blockIdx.x);
+    const int tile = select_matrix(mt, m, y, bias);
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int nl = lane & 15;
@@ -2049,27 +2030,15 @@ inline int narrow_workgroups(int64_t M, int rows, int mi, int cus) {
     return full + 2 * (tiles - full);
 }
 
-// Workgroups of an XL = 2 decode launch: as many as the LDS
-// holds at once (x staged whole beside the reduction buffer), at most one
-// per row tile.
-inline int decode_staged_grid(size_t xbytes, int tiles, int cus) {
-    if (!EBK_DECODE_PERSIST) return tiles;
-    const size_t per_wg = xbytes + static_cast<size_t>(kDecodeWaves) * 64 * 16;
-    const int fit = static_cast<int>(std::min<size_t>(4, std::max<size_t>(1, kLdsPerCu / per_wg)));
-    return std::min(tiles, fit * cus);
-}
-
 // Whether linear_decode_kernel finishes 16 < M <= kDecodeMaxM rows before
 // the prefill kernel.  The decode kernel reads the weights once, but every
 // row tile re-reads all M x K activations from L2; the 64-row prefill tiles
 // are few at these M, so their time is one tile's walk over K per round.
 // Fitted on MI355X at b = 10 (us): decode ~ max(weight bytes at 5 TB/s,
-// W * M * K * 2 at R) + 2, with W the workgroups that stage or re-read x
-// (one per row tile; for x staged whole beyond 32 KB, the workgroups that
-// fit at once) and R the rate of the activation path the decode launch
-// takes (6.5 TB/s staged whole up to 32 KB, 5.2 TB/s staged in LDS beyond
-// that, 7.5 TB/s read per lane from L2); prefill ~ (3 + 0.005 K) per
-// round.  Measured (decode against prefill, us):
+// rtiles * M * K * 2 at R) + 2, with R the rate of the activation path the
+// decode launch takes (6.5 TB/s staged whole up to 32 KB, 5.2 TB/s staged
+// in LDS beyond that, 7.5 TB/s read per lane from L2); prefill ~
+// (3 + 0.005 K) per round.  Measured (decode against prefill, us):
 // 4096 x 4096 M = 64 19.8 / 24.6; 11008 x 4096 M = 17 20.5 / 23.3,
 // M = 24 25.6 / 23.7; 14336 x 4096 M = 17 26.1 / 24.5; 4096 x 11008
 // M = 64 46.8 / 61.1.
@@ -2077,11 +2046,8 @@ inline bool prefer_decode(int64_t M, const DevMatrix& m, int cus) {
     if (M <= 16) return true;
     if (M > kDecodeMaxM) return false;
     const double wbytes = static_cast<double>(m.rows) * m.cols * (m.bits == 16 ? 16 : m.bits) / 8.0;
+    const double xbytes = static_cast<double>(m.rtiles) * static_cast<double>(M) * m.cols * 2.0;
     const double staged = static_cast<double>(M) * m.spr * kTileGroups * kGroup * 2.0;   // as launch_decode
-    const int xwg = (staged > kXLdsBytes && staged <= kXLdsDirectBytes)
-                        ? decode_staged_grid(static_cast<size_t>(staged), m.rtiles, cus)
-                        : m.rtiles;
-    const double xbytes = static_cast<double>(xwg) * static_cast<double>(M) * m.cols * 2.0;
     const double rate = staged <= kXLdsBytes ? 6.5e6
                         : (staged <= kXLdsDirectBytes || M <= 32) ? 5.2e6 : 7.5e6;
     const double t_decode = std::max(wbytes / 5.0e6, xbytes / rate) + 2.0;
@@ -2137,25 +2103,21 @@ void launch_decode(const DevMatrix& m, const uint16_t* x, int64_t M, uint16_t* y
     const size_t xbytes = static_cast<size_t>(M) * m.spr * kTileGroups * kGroup * 2;
     if (xbytes <= static_cast<size_t>(kXLdsBytes)) {
         hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, 1, MB>), dim3(tiles),
-                           dim3(64 * kDecodeWaves), xbytes, s, m, x, static_cast<int>(M), y, bias, xvec, mt, tiles);
+                           dim3(64 * kDecodeWaves), xbytes, s, m, x, static_cast<int>(M), y, bias, xvec, mt);
     } else if (xvec == 2 && xbytes <= static_cast<size_t>(kXLdsDirectBytes)) {
-        // as many workgroups as the LDS holds at once (the reduction buffer
-        // beside the staged x), each looping over row tiles
-        const int grid = decode_staged_grid(xbytes, tiles, device_cu_count());
-        hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, 2, MB>), dim3(grid),
-                           dim3(64 * kDecodeWaves), xbytes, s, m, x, static_cast<int>(M), y, bias, xvec, mt, tiles);
+        hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, 2, MB>), dim3(tiles),
+                           dim3(64 * kDecodeWaves), xbytes, s, m, x, static_cast<int>(M), y, bias, xvec, mt);
     } else if (MB <= 2 && xvec == 2 && EBK_DECODE_CHUNKED) {
         if constexpr (MB <= 2) {
             constexpr int CT = MB == 1 ? 16 : 8;     // as in the kernel
             const int64_t Mp = (M + 32 / CT - 1) / (32 / CT) * (32 / CT);
             const size_t lds = static_cast<size_t>(2 * Mp * CT * kTileGroups * kGroup * 2);
             hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, 3, MB>), dim3(tiles),
-                               dim3(64 * kDecodeWaves), lds, s, m, x, static_cast<int>(M), y, bias, xvec, mt,
-                               tiles);
+                               dim3(64 * kDecodeWaves), lds, s, m, x, static_cast<int>(M), y, bias, xvec, mt);
         }
     } else {
         hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, 0, MB>), dim3(tiles),
-                           dim3(64 * kDecodeWaves), 0, s, m, x, static_cast<int>(M), y, bias, xvec, mt, tiles);
+                           dim3(64 * kDecodeWaves), 0, s, m, x, static_cast<int>(M), y, bias, xvec, mt);
     }
 }
 

@@ -706,13 +706,12 @@ def test_activations_beyond_4_gib_use_64_bit_addressing(native):
 
 @pytest.mark.parametrize("M", [8, 16, 17])
 @pytest.mark.parametrize("rows", [11000, 14336])
-def test_decode_workgroups_loop_over_row_tiles(native, rows, M):
-    """With x staged whole in LDS beyond 32 KB (M x 4096 here), the decode
-    launch holds only the workgroups that fit on the chip at once and each
-    loops over row tiles, staging x once.  With 688 or 896 row tiles (the
-    last one partial at 11000 rows) every workgroup takes several.  All rows
-    match the fp32 product of the decoded weights, and the first and last 24
-    rows the fp64 oracle."""
+def test_decode_with_more_row_tiles_than_cus(native, rows, M):
+    """Decode with x staged whole in LDS beyond 32 KB (M x 4096 here, one
+    workgroup per CU at a time) over 688 or 896 row tiles, several rounds of
+    workgroups, the last tile partial at 11000 rows.  All rows match the
+    fp32 product of the decoded weights, and the first and last 24 rows the
+    fp64 oracle."""
     cols, b = 4096, 10
     rng = np.random.default_rng(rows + M)
     q = _codes(rng, rows, cols, b)
@@ -731,11 +730,10 @@ def test_decode_workgroups_loop_over_row_tiles(native, rows, M):
 
 
 @pytest.mark.parametrize("M", [16, 17])
-def test_multi_matrix_decode_loops_over_tiles_of_every_matrix(native, M):
-    """A multi-matrix decode launch (Gate/Up: two 11008 x 4096 matrices and a
-    third of another width) whose workgroups loop over row tiles crossing
-    from one matrix to the next returns each matrix's own forward bit for
-    bit."""
+def test_multi_matrix_decode_over_large_matrices(native, M):
+    """A multi-matrix decode launch over 1632 row tiles (Gate/Up: two
+    11008 x 4096 matrices and a 4096 x 4096 one) with x staged whole returns
+    each matrix's own forward bit for bit."""
     cols = 4096
     rng = np.random.default_rng(900 + M)
     mats = []
