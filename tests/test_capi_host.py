@@ -147,6 +147,31 @@ def test_analyzer_bit_exact_against_oracle():
     assert ours["selectedError"] <= 0.02
 
 
+def test_analyzer_closed_forms():
+    """eb_analyze on the cases whose errors mathematics fixes (dyadic weights:
+    exact zeros where the decode reproduces w; one nonzero per row: float64
+    closed form; all-zero matrix: all zeros, b = 3 selected)."""
+    from analyzer_cases import WIDTHS, decoded_equals_weights, dyadic_case, one_hot_case, one_hot_expected
+
+    w, x = dyadic_case()
+    got = {a["bits"]: a for a in native.analyze(w, x, 0.0)["candidates"]}
+    for b in WIDTHS:
+        assert (got[b]["fullPrecisionError"] == 0.0) == decoded_equals_weights(w, b), b
+    assert got[4]["hardwareNativeError"] == 0.0 and got[7]["hardwareNativeError"] == 0.0
+    assert native.analyze(w, x, 0.0)["selectedBits"] == 4
+
+    w, x, cols_of = one_hot_case()
+    got = {a["bits"]: a for a in native.analyze(w, x, 0.01)["candidates"]}
+    for b in WIDTHS:
+        hw, full = one_hot_expected(w, x, cols_of, b)
+        np.testing.assert_allclose(got[b]["hardwareNativeError"], hw, rtol=1e-12, atol=0)
+        np.testing.assert_allclose(got[b]["fullPrecisionError"], full, rtol=1e-12, atol=0)
+
+    zero = native.analyze(np.zeros((6, 10), np.float32), np.ones((3, 10), np.float32), 0.0)
+    assert all(a["error"] == 0.0 for a in zero["candidates"])
+    assert zero["selectedBits"] == 3 and zero["selectedError"] == 0.0
+
+
 def test_analyzer_matches_pure_python_golden(golden):
     ours = native.analyze(golden["analyze_w"], golden["analyze_calib"], 0.01)
     for a, (b, hw, fp) in zip(ours["candidates"], golden["analyze_errors"]):

@@ -186,6 +186,63 @@ def test_analyzer_matches_pure_python_restatement(golden):
         ora.select(out, float("nan"))
 
 
+def test_analyzer_dyadic_weights_are_exact_where_the_decode_is():
+    """Dyadic weights: an error is exactly 0 where the decoded weights equal w
+    (b = 4, 7, 10, 13 among them, since their qmax is a multiple of 7) and
+    positive elsewhere.  A dropped fp16 rounding, a wrong scale or a wrong
+    reference output makes a zero positive or a positive zero."""
+    from analyzer_cases import WIDTHS, decoded_equals_weights, dyadic_case
+
+    w, x = dyadic_case()
+    out = {a["bits"]: a for a in ora.analyze(w, x)}
+    assert tuple(out) == WIDTHS
+    exact = {b for b in WIDTHS if decoded_equals_weights(w, b)}
+    assert {4, 7, 10, 13, 16} <= exact
+    assert not {3, 5, 6, 8} & exact
+    for b in WIDTHS:
+        full = out[b]["fullPrecisionError"]
+        assert (full == 0.0) == (b in exact), (b, full)
+    # integer-dot outputs (b <= 8) are exact where q = (qmax/7)*k and s carries
+    # the 1/(qmax/7): b = 4 (s = 2^-7) and b = 7 (9*fp32(2^-7/9) rounds to 2^-7)
+    for b in (4, 7):
+        assert out[b]["hardwareNativeError"] == 0.0
+    for b in (3, 5, 6, 8):
+        assert out[b]["hardwareNativeError"] > 0.0
+    for b in range(9, 17):
+        assert out[b]["hardwareNativeError"] == out[b]["fullPrecisionError"]
+    assert ora.select(list(out.values()), 0.0) == 1       # b = 4 is the first exact width
+
+
+def test_analyzer_all_zero_matrix():
+    w = np.zeros((6, 10), np.float32)
+    x = np.random.default_rng(1).normal(size=(4, 10)).astype(np.float32)
+    out = ora.analyze(w, x)
+    for a in out:
+        assert a["hardwareNativeError"] == 0.0 and a["fullPrecisionError"] == 0.0
+        b = a["bits"]
+        assert a["storageBytes"] == (120 if b == 16 else (60 * b + 7) // 8 + 24)
+    assert np.array_equal(ora.row_scales(w, 8), np.ones(6, np.float32))
+    assert out[ora.select(out, 0.0)]["bits"] == 3
+
+
+def test_analyzer_one_nonzero_per_row_closed_form():
+    """Every output is one product, so each error is a float64 closed form of
+    the decoded weights; a transposed output index, a missing square root or
+    a reference built from unrounded weights all move it."""
+    from analyzer_cases import WIDTHS, one_hot_case, one_hot_expected
+
+    w, x, cols_of = one_hot_case()
+    out = {a["bits"]: a for a in ora.analyze(w, x)}
+    for b in WIDTHS:
+        hw, full = one_hot_expected(w, x, cols_of, b)
+        np.testing.assert_allclose(out[b]["hardwareNativeError"], hw, rtol=1e-12, atol=0)
+        np.testing.assert_allclose(out[b]["fullPrecisionError"], full, rtol=1e-12, atol=0)
+        assert out[b]["error"] == max(out[b]["hardwareNativeError"], out[b]["fullPrecisionError"])
+    # the integer-dot output carries the unrounded weight (q*s = w to float32
+    # precision) while the reference carries fp16(w): positive error at b <= 8
+    assert all(out[b]["hardwareNativeError"] > 0 for b in range(3, 9))
+
+
 # -- MLB4 / FNV ------------------------------------------------------------------------
 
 def test_fnv1a64_published_vectors(golden):
