@@ -195,11 +195,13 @@ int eb_forward_multi(const eb_matrix* const* ms, int count, const void* x_f16, i
  * (fp32, device), it writes partials [ceil(rows / EB_ANALYZE_TILE_ROWS)]
  * [EB_ANALYZE_SUMS] (fp32, device): per tile of weight rows, sum |ref|^2,
  * then sum |full_b - ref|^2 for b = 3..15, then sum |hw_b - ref|^2 for
- * b = 3..8, where ref = fp16(x . w^T), full_b = fp16(x . fp16(q_b s_b)^T) and
+ * b = 3..12, where ref = fp16(x . w^T), full_b = fp16(x . fp16(q_b s_b)^T) and
  * hw_b = fp16((x . q_b^T) s_b).  The tiles' sums give the reference's relL2
- * errors (core.py:103-108); more calibration rows are more calls.  Stream-
- * ordered, allocates nothing. */
-enum { EB_ANALYZE_TILE_ROWS = 16, EB_ANALYZE_MAX_SAMPLES = 32, EB_ANALYZE_SUMS = 20 };
+ * errors (core.py:103-108); more calibration rows are more calls.  The
+ * reference measures hw_b only for b <= 8 because it runs W16A16 above; this
+ * runtime's hardwareNative runs the integer-code product up to b = 12, so
+ * its error is measured there too.  Stream-ordered, allocates nothing. */
+enum { EB_ANALYZE_TILE_ROWS = 16, EB_ANALYZE_MAX_SAMPLES = 32, EB_ANALYZE_SUMS = 24 };
 int eb_analyze_widths_device(const void* w_f16, int64_t rows, int64_t cols, const void* x_f16, int64_t samples,
                              const float* max_abs, float* partials, void* stream);
 
@@ -225,11 +227,12 @@ int eb_packed_linear(const void* x, int x_dtype, int64_t M, const uint8_t* packe
  * vendor GEMM): the output tile shape of the prefill route (M > 16, b <= 15,
  * hardwareNative or fullPrecision).  EB_PREFILL_TILES_AUTO (the default)
  * picks the shape with the fewer estimated rounds over the GPU's compute
- * units; NARROW forces 128 x 256 tiles; WIDE forces 256 x 256 tiles where M
- * and rows are both at least 256.  Results agree within the output
- * tolerance either way; the sum order differs.  Process-wide, read at each
- * launch. */
-enum { EB_PREFILL_TILES_AUTO = 0, EB_PREFILL_TILES_NARROW = 1, EB_PREFILL_TILES_WIDE = 2 };
+ * units; NARROW forces 128 x 256 tiles; WIDE forces 256 x 256 tiles with
+ * four waves where M and rows are both at least 256, WIDE8 the same tiles
+ * with eight waves.  Results agree within the output tolerance either way;
+ * the sum order differs.  Process-wide, read at each launch. */
+enum { EB_PREFILL_TILES_AUTO = 0, EB_PREFILL_TILES_NARROW = 1, EB_PREFILL_TILES_WIDE = 2,
+       EB_PREFILL_TILES_WIDE8 = 3 };
 int eb_set_prefill_tiles(int mode);
 
 /* ---- host codec (the packer inside the RuntimeMatrix constructors) --------- */

@@ -1085,8 +1085,9 @@ int eb_packed_linear(const void* x, int x_dtype, int64_t M, const uint8_t* packe
 
 int eb_set_prefill_tiles(int mode) {
     return guarded([&] {
-        require(mode == EB_PREFILL_TILES_AUTO || mode == EB_PREFILL_TILES_NARROW || mode == EB_PREFILL_TILES_WIDE,
-                "prefill tile mode must be auto (0), narrow (1) or wide (2)");
+        require(mode == EB_PREFILL_TILES_AUTO || mode == EB_PREFILL_TILES_NARROW || mode == EB_PREFILL_TILES_WIDE ||
+                    mode == EB_PREFILL_TILES_WIDE8,
+                "prefill tile mode must be auto (0), narrow (1), wide (2) or wide with eight waves (3)");
         ebk::set_prefill_tiles(mode);
     });
 }

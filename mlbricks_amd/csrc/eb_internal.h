@@ -1,5 +1,5 @@
 // Internal interface between the host runtime (eb_host.cpp) and the gfx950
-// kernels (eb_kernels.hip).  Not installed; the public ABI is include/elasticbit.h.
+// kernels (eb_kernels.hip, eb_prefill.hip, eb_analyze.hip).  Not installed; the public ABI is include/elasticbit.h.
 //
 // Device execution layout ("bit planes" in lane-ordered tiles)
 // -------------------------------------------------------------
@@ -82,10 +82,7 @@ struct DevMatrixOut {
 // with one load instead of two.  Measured on MI355X at M = 1 and 4:
 // 11008 x 4096 b = 11 13.66 -> 13.23 us, b = 15 0.4-2% faster; b = 3 (whose
 // only planes these are) was no faster and keeps them apart.
-#ifndef EBK_MERGED_TAIL
-#define EBK_MERGED_TAIL 1
-#endif
-constexpr bool merged_tail(int bits) { return EBK_MERGED_TAIL && bits >= 7 && bits != 16 && (bits & 3) == 3; }
+constexpr bool merged_tail(int bits) { return bits >= 7 && bits != 16 && (bits & 3) == 3; }
 
 // Bytes of the plane of width `width` (8, 4, 2, 1; 16 = raw fp16) for
 // `groups` slots (rtiles * spr * 64); 0 when b has no such plane (or keeps
@@ -140,16 +137,24 @@ hipError_t launch_linear_multi(const DevMatrix* ms, int count, bool exact_w16, c
 
 // Fused width search (eb_analyze.hip): per tile of kAnalyzeTileRows weight
 // rows, kAnalyzeSums partial sums (|ref|^2, then |full_b - ref|^2 for
-// b = 3..15, then |hw_b - ref|^2 for b = 3..8) over up to
+// b = 3..15, then |hw_b - ref|^2 for b = 3..12) over up to
 // kAnalyzeMaxSamples calibration rows.
 constexpr int kAnalyzeTileRows = 16;
 constexpr int kAnalyzeMaxSamples = 32;
-constexpr int kAnalyzeSums = 20;
+constexpr int kAnalyzeSums = 24;
 hipError_t launch_analyze_widths(const uint16_t* w, int N, int K, const uint16_t* x, int S, const float* max_abs,
                                  float* partials, hipStream_t stream);
 
-// Prefill tile shape: 0 auto, 1 128 x 256, 2 256 x 256 (process-wide).
+// Prefill tile shape: 0 auto, 1 128 x 256, 2 256 x 256 with four waves,
+// 3 256 x 256 with eight waves (process-wide).
 void set_prefill_tiles(int mode);
+
+// 256 x 256 prefill tiles with eight waves (eb_prefill.hip).  mode: 0
+// integer-code dot product (b <= 12), 1 decoded fp16 weights, 2 raw fp16
+// weights (b = 16).  Requires M >= 1, cols % 8 == 0, a 16-byte aligned x,
+// M * cols * 2 below 4 GiB and planes below 4 GiB.
+hipError_t launch_prefill_pp(const DevMatrix& m, int mode, const uint16_t* x, int64_t M, uint16_t* y,
+                             const uint16_t* bias, hipStream_t stream);
 
 // Legacy flat-group op (bolt/ops_cuda.cu:2708-2795).
 hipError_t launch_packed_linear(const void* x, int x_dtype, int64_t M, const uint8_t* packed,

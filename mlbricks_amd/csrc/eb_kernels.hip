@@ -8,222 +8,15 @@
 //   W16A16 output       y = fp16_rn(sum_c w_rc * x_c)               (:635-647)
 //   bias                y = fp16_rn(y + bias), as torch adds it     (core.py:457-459)
 // All sums accumulate in fp32 on the matrix cores.
-#include "eb_internal.h"
+#include "eb_device.h"
 
 #include <atomic>
 #include <type_traits>
-
-#ifndef W_ILV
-#define W_ILV 0
-#endif
 
 #include <hip/hip_runtime.h>
 
 namespace ebk {
 namespace {
-
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-typedef float floatx4 __attribute__((ext_vector_type(4)));
-
-// ---------------------------------------------------------------------------
-// plane geometry
-// ---------------------------------------------------------------------------
-
-template <int B>
-struct Planes {
-    static_assert(B >= 3 && B <= 15, "compressed widths only");
-    static constexpr bool h8 = (B & 8) != 0;
-    static constexpr bool h4 = (B & 4) != 0;
-    static constexpr bool h2 = (B & 2) != 0;
-    static constexpr bool h1 = (B & 1) != 0;
-    static constexpr bool h21 = merged_tail(B);        // 2- and 1-bit words in one 12-byte slot
-    static constexpr int off4 = h8 ? 8 : 0;           // bit offset of each plane in u
-    static constexpr int off2 = off4 + (h4 ? 4 : 0);
-    static constexpr int off1 = off2 + (h2 ? 2 : 0);
-    static constexpr int qmax = (1 << (B - 1)) - 1;
-};
-
-// Raw plane words of one 32-code group.
-template <int B>
-struct Raw {
-    uint32_t d8[8];
-    uint32_t d4[4];
-    uint32_t d2[2];
-    uint32_t d1;
-};
-
-template <int B>
-__device__ __forceinline__ void raw_zero(Raw<B>& r) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) r.d8[i] = 0u;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r.d4[i] = 0u;
-    r.d2[0] = r.d2[1] = 0u;
-    r.d1 = 0u;
-}
-
-template <int B>
-__device__ __forceinline__ void raw_load(const DevMatrix& m, size_t g, Raw<B>& r) {
-    using P = Planes<B>;
-    if constexpr (P::h8) {
-        const uint4* p = reinterpret_cast<const uint4*>(m.p8) + 2 * g;
-        const uint4 a = p[0];
-        const uint4 b = p[1];
-        r.d8[0] = a.x; r.d8[1] = a.y; r.d8[2] = a.z; r.d8[3] = a.w;
-        r.d8[4] = b.x; r.d8[5] = b.y; r.d8[6] = b.z; r.d8[7] = b.w;
-    }
-    if constexpr (P::h4) {
-        const uint4 a = reinterpret_cast<const uint4*>(m.p4)[g];
-        r.d4[0] = a.x; r.d4[1] = a.y; r.d4[2] = a.z; r.d4[3] = a.w;
-    }
-    if constexpr (P::h21) {
-        const uint3 a = *reinterpret_cast<const uint3*>(m.p2 + g * 12);
-        r.d2[0] = a.x; r.d2[1] = a.y; r.d1 = a.z;
-    } else {
-        if constexpr (P::h2) {
-            const uint2 a = reinterpret_cast<const uint2*>(m.p2)[g];
-            r.d2[0] = a.x; r.d2[1] = a.y;
-        }
-        if constexpr (P::h1) {
-            r.d1 = reinterpret_cast<const uint32_t*>(m.p1)[g];
-        }
-    }
-}
-
-// raw_load with a 32-bit slot index: the planes of one matrix stay below
-// 4 GiB, so each address is a scalar base plus a 32-bit vector byte offset
-// (the saddr form of global_load) instead of 64-bit vector arithmetic.
-template <int B>
-__device__ __forceinline__ void raw_load32(const DevMatrix& m, uint32_t g, Raw<B>& r) {
-    using P = Planes<B>;
-    if constexpr (P::h8) {
-        const uint8_t* p = m.p8 + g * 32u;
-        const uint4 a = *reinterpret_cast<const uint4*>(p);
-        const uint4 b = *reinterpret_cast<const uint4*>(p + 16);
-        r.d8[0] = a.x; r.d8[1] = a.y; r.d8[2] = a.z; r.d8[3] = a.w;
-        r.d8[4] = b.x; r.d8[5] = b.y; r.d8[6] = b.z; r.d8[7] = b.w;
-    }
-    if constexpr (P::h4) {
-        const uint4 a = *reinterpret_cast<const uint4*>(m.p4 + g * 16u);
-        r.d4[0] = a.x; r.d4[1] = a.y; r.d4[2] = a.z; r.d4[3] = a.w;
-    }
-    if constexpr (P::h21) {
-        const uint3 a = *reinterpret_cast<const uint3*>(m.p2 + g * 12u);
-        r.d2[0] = a.x; r.d2[1] = a.y; r.d1 = a.z;
-    } else {
-        if constexpr (P::h2) {
-            const uint2 a = *reinterpret_cast<const uint2*>(m.p2 + g * 8u);
-            r.d2[0] = a.x; r.d2[1] = a.y;
-        }
-        if constexpr (P::h1) {
-            r.d1 = *reinterpret_cast<const uint32_t*>(m.p1 + g * 4u);
-        }
-    }
-}
-
-// Quad d (codes 4d..4d+3) as byte lanes: lo = bits 0..7 of each u, hi = bits 8+.
-template <int B>
-__device__ __forceinline__ void quad_bytes(const Raw<B>& r, int d, uint32_t& lo, uint32_t& hi) {
-    using P = Planes<B>;
-    constexpr int base = P::h8 ? 8 : 0;
-    uint32_t small = 0u;
-    if constexpr (P::h4) small |= ((r.d4[d >> 1] >> (4 * (d & 1))) & 0x0F0F0F0Fu) << (P::off4 - base);
-    if constexpr (P::h2) small |= ((r.d2[d >> 2] >> (2 * (d & 3))) & 0x03030303u) << (P::off2 - base);
-    if constexpr (P::h1) small |= ((r.d1 >> d) & 0x01010101u) << (P::off1 - base);
-    if constexpr (P::h8) {
-        lo = r.d8[d];
-        hi = small;
-    } else {
-        lo = small;
-        hi = 0u;
-    }
-}
-
-__device__ __forceinline__ uint32_t pack_h2(_Float16 a, _Float16 b) {
-    half2v v = {a, b};
-    return __builtin_bit_cast(uint32_t, v);
-}
-
-// Exact fp16 codes q for one quad, b <= 12 (every |q| <= 2047 is an fp16
-// integer).  The low ten bits of u become the mantissa of 1024 + u_lo
-// (fp16 0x6400 | u_lo).  For b <= 10 that is all of u, and 1024 + qmax is
-// subtracted.  For b = 11, 12 the subtraction is 2047 = 1024 + 1023, and the
-// top bits t = u >> 10 add 1024 t + 1023 - qmax, looked up with one
-// v_perm_b32 as fp16 high bytes (the low bytes are zero): b = 11, t in
-// {0, 1}: {0, 1024}; b = 12, t in {0..3}: {-1024, 0, 1024, 2048}.  Every
-// partial result is an integer of magnitude at most 2048, so each fp16 step
-// is exact.
-template <int B>
-__device__ __forceinline__ void quad_q(uint32_t lo, uint32_t hi, uint32_t& w0, uint32_t& w1) {
-    static_assert(B <= 12, "fp16 holds the codes exactly only up to 12 bits");
-    // the low two bits of each hi byte are bits 8..9 of u; OR-ing in the
-    // exponent byte 0x64 is then a bit-field insert
-    const uint32_t H = (B <= 10 ? hi : (hi & 0x03030303u)) | 0x64646464u;
-    const uint32_t a = __builtin_amdgcn_perm(H, lo, 0x05010400u);  // [lo0 H0 lo1 H1]
-    const uint32_t b = __builtin_amdgcn_perm(H, lo, 0x07030602u);  // [lo2 H2 lo3 H3]
-    constexpr _Float16 off = static_cast<_Float16>(B <= 10 ? 1024 + Planes<B>::qmax : 2047);
-    const half2v o = {off, off};
-    half2v q01 = __builtin_bit_cast(half2v, a) - o;
-    half2v q23 = __builtin_bit_cast(half2v, b) - o;
-    if constexpr (B > 10) {
-        // fp16 high bytes of 1024 t + 1023 - qmax for t = 0..3
-        constexpr uint32_t lut = B == 11 ? 0x00006400u : 0x686400E4u;
-        const uint32_t t = (hi >> 2) & (B == 11 ? 0x01010101u : 0x03030303u);
-        const uint32_t tb = __builtin_amdgcn_perm(0u, lut, t);                   // [L(t0) L(t1) L(t2) L(t3)]
-        const uint32_t h01 = __builtin_amdgcn_perm(0u, tb, 0x01040004u);         // [0 L(t0) 0 L(t1)]
-        const uint32_t h23 = __builtin_amdgcn_perm(0u, tb, 0x03040204u);         // [0 L(t2) 0 L(t3)]
-        q01 = q01 + __builtin_bit_cast(half2v, h01);
-        q23 = q23 + __builtin_bit_cast(half2v, h23);
-    }
-    w0 = __builtin_bit_cast(uint32_t, q01);
-    w1 = __builtin_bit_cast(uint32_t, q23);
-}
-
-// a * b rounded to fp32.  The reference rounds products to fp32 before the
-// fp16 rounding (__float2half_rn(q * s)); left alone the compiler fuses
-// fmul + fptrunc into one v_fma_mix with a single rounding, which differs on
-// rare double-rounding ties.  The empty asm hides the product from that
-// combine and emits no instruction.
-__device__ __forceinline__ float mul_f32(float a, float b) {
-    float p = a * b;
-    __asm__("" : "+v"(p));
-    return p;
-}
-
-// Exact decoded weights fp16_rn(f32(q) * s) for one quad (any b <= 15).
-template <int B>
-__device__ __forceinline__ void quad_w(uint32_t lo, uint32_t hi, float s, uint32_t& w0, uint32_t& w1) {
-    _Float16 h[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int u = static_cast<int>(((lo >> (8 * j)) & 0xFFu) | (((hi >> (8 * j)) & 0xFFu) << 8));
-        const float q = static_cast<float>(u - Planes<B>::qmax);
-        h[j] = static_cast<_Float16>(mul_f32(q, s));
-    }
-    w0 = pack_h2(h[0], h[1]);
-    w1 = pack_h2(h[2], h[3]);
-}
-
-enum Mode { kModeQ = 0, kModeW = 1, kModeRaw = 2 };
-
-// Decode the 8 codes [8t, 8t+8) of a group into an MFMA operand.
-template <int B, int MODE>
-__device__ __forceinline__ half8 decode8(const Raw<B>& r, int t, float s) {
-    uint32_t w[4];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        uint32_t lo, hi;
-        quad_bytes<B>(r, 2 * t + h, lo, hi);
-        if constexpr (MODE == kModeQ) {
-            quad_q<B>(lo, hi, w[2 * h], w[2 * h + 1]);
-        } else {
-            quad_w<B>(lo, hi, s, w[2 * h], w[2 * h + 1]);
-        }
-    }
-    uint4 v = {w[0], w[1], w[2], w[3]};
-    return __builtin_bit_cast(half8, v);
-}
 
 // ---------------------------------------------------------------------------
 // bit-exact canonical extraction (elasticbit_runtime.cu:188-206)
@@ -421,73 +214,6 @@ __global__ void materialize_kernel(DevMatrix m, uint16_t* __restrict__ out, uint
     store_group(out + static_cast<uint64_t>(row) * m.cols, col0, m.cols, w);
 }
 
-// ---------------------------------------------------------------------------
-// shared pieces of the linear kernels
-// ---------------------------------------------------------------------------
-
-// fp16 bits -> float and float -> fp16 bits (round to nearest even).
-__device__ __forceinline__ float h2f(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
-__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f)); }
-
-// Output epilogue: integer-dot scale, fp16 rounding, then torch-style bias add.
-template <int MODE>
-__device__ __forceinline__ uint16_t epilogue(float acc, float s, bool has_bias, uint16_t bias_bits) {
-    uint16_t y = f2h(MODE == kModeQ ? mul_f32(acc, s) : acc);
-    if (has_bias) y = f2h(h2f(y) + h2f(bias_bits));
-    return y;
-}
-
-// Load the 32 activations x[row][k0 .. k0+32) as four 8-half MFMA operands,
-// zero beyond `cols`.  vec: cols % 8 == 0 and x 16-byte aligned.
-__device__ __forceinline__ void load_x32(const uint16_t* __restrict__ xrow, int k0, int cols, bool vec,
-                                         half8 (&a)[4]) {
-    if (vec && k0 + kGroup <= cols) {
-        const uint4* p = reinterpret_cast<const uint4*>(xrow + k0);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) a[t] = __builtin_bit_cast(half8, p[t]);
-    } else {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int k = k0 + 8 * t + i;
-                a[t][i] = k < cols ? __builtin_bit_cast(_Float16, xrow[k]) : static_cast<_Float16>(0.0f);
-            }
-        }
-    }
-}
-
-// An LDS address as the address-space-3 pointer global_load_lds takes.  The
-// explicit cast at the call matters: without it hipcc's host pass silently
-// drops the launch stub of a kernel template that passes an LDS array
-// expression of dependent type to the builtin (and a __device__ helper doing
-// the cast has the same effect).
-typedef __attribute__((address_space(3))) void* lds_void_ptr;
-
-// Workgroup barrier for the direct-to-LDS pipeline.  __syncthreads() opens
-// with a release fence, which waits for every outstanding vector load --
-// including the prefetch that should stay in flight across the barrier.
-// The caller waits for the loads the next step reads (wait_vmcnt) and the
-// barrier keeps only the acquire side.  Prior LDS reads have all returned:
-// their MFMAs consumed them.
-__device__ __forceinline__ void barrier_after_wait() {
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-}
-
-// s_waitcnt with only the LDS / scalar-memory counter constrained.
-template <int N>
-__device__ __forceinline__ void wait_lgkmcnt() {
-    static_assert(N >= 0 && N < 16, "lgkmcnt is a 4-bit counter");
-    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4) | (N << 8));
-}
-
-// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 
 // ---------------------------------------------------------------------------
 // decode kernel, M <= 64: one workgroup owns one row tile (16 weight rows);
@@ -518,57 +244,6 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 constexpr int kXLdsBytes = 32768;
 constexpr int kXLdsDirectBytes = 147456;   // 16 rows of 4608 halves
-
-// One group's weight bits as held in registers between load and decode.
-template <int B, int MODE>
-struct GroupBits {
-    Raw<B> r;
-    __device__ __forceinline__ void load(const DevMatrix& m, size_t g) { raw_load<B>(m, g, r); }
-    // Copy of the planes width B has (the others are never written).
-    __device__ __forceinline__ void copy_from(const GroupBits& o) {
-        using P = Planes<B>;
-        if constexpr (P::h8) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) r.d8[i] = o.r.d8[i];
-        }
-        if constexpr (P::h4) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) r.d4[i] = o.r.d4[i];
-        }
-        if constexpr (P::h2) {
-            r.d2[0] = o.r.d2[0];
-            r.d2[1] = o.r.d2[1];
-        }
-        if constexpr (P::h1) r.d1 = o.r.d1;
-    }
-    __device__ __forceinline__ void load32(const DevMatrix& m, uint32_t g) { raw_load32<B>(m, g, r); }
-    __device__ __forceinline__ half8 operand(int t, float s) const { return decode8<B, MODE>(r, t, s); }
-};
-
-template <int B>
-struct GroupBits<B, kModeRaw> {
-    uint4 w[4];
-    __device__ __forceinline__ void load(const DevMatrix& m, size_t g) {
-        const uint4* p = reinterpret_cast<const uint4*>(m.w16 + g * kGroup);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) w[t] = p[t];
-    }
-    __device__ __forceinline__ void load32(const DevMatrix& m, uint32_t g) { load(m, g); }
-    __device__ __forceinline__ void copy_from(const GroupBits& o) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) w[t] = o.w[t];
-    }
-    __device__ __forceinline__ half8 operand(int t, float) const { return __builtin_bit_cast(half8, w[t]); }
-};
-
-// Vector-memory instructions one GroupBits::load issues.
-template <int B, int MODE>
-struct GroupLoads {
-    static constexpr int value =
-        MODE == kModeRaw ? 4
-                         : (Planes<B>::h8 ? 2 : 0) + (Planes<B>::h4 ? 1 : 0) +
-                               (Planes<B>::h21 ? 1 : (Planes<B>::h2 ? 1 : 0) + (Planes<B>::h1 ? 1 : 0));
-};
 
 // Eight activations x[r][k .. k+8) as one uint4, zero at and beyond `cols`.
 __device__ __forceinline__ uint4 load_x8(const uint16_t* __restrict__ x, int r, int k, int cols, bool vec) {
@@ -1144,11 +819,8 @@ __global__ __launch_bounds__(256) void linear_gemm_kernel(
 //    activation and weight blocks in that XCD's L2.
 // ---------------------------------------------------------------------------
 
-typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kPN = 256;                   // weight rows per workgroup (4 waves x 64)
-constexpr int kPK = kTileGroups * kGroup;  // 128 columns per step
-constexpr int kPRow = kPK * 2;             // bytes per staged activation row
 constexpr int kPGroupM = 4;                // activation blocks per tile-order group
 
 // Vector-memory instructions one GroupBits::load32 issues (kModeQ / kModeW).
@@ -1524,23 +1196,18 @@ __global__ __launch_bounds__(256 * KS) void linear_prefill_kernel(
 // Widths the wide kernel takes: every packed width (b = 11..15 measured
 // 16-23% faster than linear_prefill_kernel at 14336 x 4096 M = 2048, and
 // spill-free with the ring of three half steps).
-#ifndef EBK_WIDE_MAX_BITS
-#define EBK_WIDE_MAX_BITS 15
-#endif
+constexpr int kWideMaxBits = 15;
 constexpr int kWRows = 256;                 // activation rows per workgroup
 constexpr int kWN = 256;                    // weight rows per workgroup (4 waves x 64)
 constexpr int kWHalfRow = kPRow / 2;        // bytes per staged row of a half step (64 columns)
 constexpr int kWHalf = kWRows * kWHalfRow;  // bytes per half-stage (32 KB)
-#ifndef EBK_WIDE_GROUP_M
-#define EBK_WIDE_GROUP_M 4
-#endif
-constexpr int kWGroupM = EBK_WIDE_GROUP_M;  // activation blocks per tile-order group
+constexpr int kWGroupM = 4;                 // activation blocks per tile-order group
 
 template <int B, int MODE>
 __global__ __launch_bounds__(256) void linear_prefill_wide_kernel(
     DevMatrix m, const uint16_t* __restrict__ x, int M, uint16_t* __restrict__ y,
     const uint16_t* __restrict__ bias, int mblocks, int nblocks, int njobs, int per_xcd) {
-    static_assert(B <= EBK_WIDE_MAX_BITS, "width beyond the wide kernel's ring");
+    static_assert(B <= kWideMaxBits, "width beyond the wide kernel's ring");
     using Bits = GroupBits<B, MODE>;
     constexpr int GL = GroupLoads<B, MODE>::value;  // vector loads per group
     __shared__ __attribute__((aligned(16))) uint8_t xs[4 * kWHalf];
@@ -1942,42 +1609,19 @@ struct MaterializeOp {
     }
 };
 
-#ifndef EBK_PREFILL_KS
-#define EBK_PREFILL_KS 2
-#endif
-#ifndef EBK_DECODE_WAVES
-#define EBK_DECODE_WAVES 8
-#endif
-#ifndef EBK_DECODE_GPL
-#define EBK_DECODE_GPL 1
-#endif
-constexpr int kPrefillKS = EBK_PREFILL_KS;
-constexpr int kDecodeWaves = EBK_DECODE_WAVES;
-constexpr int kDecodeGpl = EBK_DECODE_GPL;
+constexpr int kPrefillKS = 2;      // waves per column group of linear_prefill_kernel (K split)
+constexpr int kDecodeWaves = 8;    // waves per workgroup of linear_decode_kernel
+constexpr int kDecodeGpl = 1;      // weight tiles per wave batch of linear_decode_kernel
 // Activation rows the decode kernel takes (in blocks of 16; above, the
 // prefill kernels).
-#ifndef EBK_DECODE_MAX_M
-#define EBK_DECODE_MAX_M 64
-#endif
-constexpr int kDecodeMaxM = EBK_DECODE_MAX_M;
-// Modes the GEMV kernel takes (bit per Mode).  The decoded-fp16 mode
-// (b >= 11, fullPrecision) spends ~7 VALU instructions per code on the fp32
-// product and its rounding; at four waves per SIMD that work is exposed, and
-// linear_decode_kernel is faster for it (8.7 vs 9.6 us at 4096 x 4096 b = 15).
-#ifndef EBK_PREFILL_WIDE
-#define EBK_PREFILL_WIDE 1
-#endif
-// Raw fp16 weights (b = 16) through the prefill kernels (their B operand
-// is the stored fp16, no decode); linear_gemm_kernel otherwise.
-#ifndef EBK_PREFILL_RAW
-#define EBK_PREFILL_RAW 1
-#endif
-#ifndef EBK_GEMV_MODES
-#define EBK_GEMV_MODES ((1 << kModeQ) | (1 << kModeRaw))
-#endif
+constexpr int kDecodeMaxM = 64;
 
 // Whether linear_gemv_kernel takes an M = 1 launch (else
-// linear_decode_kernel).  Measured on MI355X at M = 1 over rotated copies:
+// linear_decode_kernel).  Not the decoded-fp16 mode (b >= 13, fullPrecision):
+// it spends ~7 VALU instructions per code on the fp32 product and its
+// rounding; at four waves per SIMD that work is exposed, and
+// linear_decode_kernel is faster for it (8.7 vs 9.6 us at 4096 x 4096
+// b = 15).  Measured on MI355X at M = 1 over rotated copies:
 // with K at most 16 tiles (2048 columns) half or more of the 16 waves idle
 // and the decode kernel is faster (4096 x 1024: 3.4-3.9 us against
 // 3.7-5.3 us; 4096 x 2048 from b = 10); at b = 11 the two are even or the
@@ -1988,7 +1632,7 @@ constexpr int kDecodeMaxM = EBK_DECODE_MAX_M;
 // (1024 x 4096).
 template <int B, int MODE>
 inline bool gemv_takes(const DevMatrix& m) {
-    if (!((EBK_GEMV_MODES >> MODE) & 1)) return false;
+    if (MODE == kModeW) return false;
     if (m.spr <= kGemvMaxSteps / 2 || m.spr > kGemvMaxSteps) return false;
     if (MODE != kModeRaw && (B == 11 || (B <= 7 && m.rtiles > 256))) return false;
     return true;
@@ -2004,13 +1648,26 @@ std::atomic<int> g_prefill_tiles{0};   // eb_set_prefill_tiles
 
 inline bool prefer_wide_tiles(int64_t M, int rows, int cus) {
     const int mode = g_prefill_tiles.load(std::memory_order_relaxed);
-    if (mode != 0) return mode == 2;
+    if (mode != 0) return mode >= 2;
     const int64_t wide = ((M + kWRows - 1) / kWRows) * ((rows + kWN - 1) / kWN);
     const int64_t narrow = ((M + 127) / 128) * ((rows + kPN - 1) / kPN);
     const double t_wide = 1.7 * static_cast<double>((wide + cus - 1) / cus);
     const int64_t rem = narrow % cus;
     const double t_narrow = static_cast<double>(narrow / cus) + (rem == 0 ? 0.0 : (2 * rem <= cus ? 0.67 : 1.0));
     return t_wide < t_narrow;
+}
+
+// Whether 256 x 256 tiles run with eight waves (eb_prefill.hip) rather than
+// four.  Measured on MI355X (us, four -> eight waves): integer-code widths
+// up to 11 gain (14336 x 4096 M = 2048 b = 10 244.5 -> 238.1, b = 7
+// 242.1 -> 233.6; 11008 x 4096 M = 2048 b = 10 230.4 -> 207.7; 4096 x 4096
+// M = 8192 256.3 -> 246.6); b = 12 (258.1 -> 262.8), the decoded-fp16
+// widths (b = 13: 296.0 -> 334.3) and raw fp16 (241.5 -> 254.1) lose, and
+// keep four waves.
+template <int B, int MODE>
+inline bool prefill_eight_waves() {
+    const int mode = g_prefill_tiles.load(std::memory_order_relaxed);
+    return mode == 3 || (mode == 0 && MODE == kModeQ && B <= 11);
 }
 
 // Tiles of linear_prefill_kernel with MI 32-row activation blocks: full
@@ -2086,13 +1743,6 @@ void launch_narrow(const DevMatrix& m, const uint16_t* x, int64_t M, uint16_t* y
     }
 }
 
-// Activations too long to stage whole (x's rows whole tiles, M <= 32) go
-// through LDS in double-buffered K chunks (XL = 3) instead of per-lane L2
-// reads.
-#ifndef EBK_DECODE_CHUNKED
-#define EBK_DECODE_CHUNKED 1
-#endif
-
 // linear_decode_kernel for M <= 16 MB rows: activations staged in LDS when
 // they fit (directly up to kXLdsDirectBytes when x's rows are whole tiles),
 // in K chunks when they do not (whole tiles, M <= 32), read per lane from
@@ -2107,7 +1757,7 @@ void launch_decode(const DevMatrix& m, const uint16_t* x, int64_t M, uint16_t* y
     } else if (xvec == 2 && xbytes <= static_cast<size_t>(kXLdsDirectBytes)) {
         hipLaunchKernelGGL((linear_decode_kernel<B, MODE, kDecodeWaves, kDecodeGpl, 2, MB>), dim3(tiles),
                            dim3(64 * kDecodeWaves), xbytes, s, m, x, static_cast<int>(M), y, bias, xvec, mt);
-    } else if (MB <= 2 && xvec == 2 && EBK_DECODE_CHUNKED) {
+    } else if (MB <= 2 && xvec == 2) {
         if constexpr (MB <= 2) {
             constexpr int CT = MB == 1 ? 16 : 8;     // as in the kernel
             const int64_t Mp = (M + 32 / CT - 1) / (32 / CT) * (32 / CT);
@@ -2147,25 +1797,21 @@ hipError_t run_linear_mode(const DevMatrix& m, const uint16_t* x, int64_t M, uin
         }
     } else if (mt.count > 1) {
         return hipErrorInvalidValue;      // the launcher splits prefill per matrix
-    } else if (B <= EBK_WIDE_MAX_BITS && (MODE != kModeRaw || EBK_PREFILL_RAW) && EBK_PREFILL_WIDE && xvec &&
-               offsets32 && M >= kWRows && m.rows >= kWN &&
+    } else if (xvec && offsets32 && M >= kWRows && m.rows >= kWN &&
                prefer_wide_tiles(M, m.rows, device_cu_count())) {
-        if constexpr (B <= EBK_WIDE_MAX_BITS && (MODE != kModeRaw || EBK_PREFILL_RAW)) {
-            const int mblocks = static_cast<int>((M + kWRows - 1) / kWRows);
-            const int nblocks = (m.rows + kWN - 1) / kWN;
-            const int jobs = mblocks * nblocks;
-            const int per_xcd = (jobs + 7) / 8;
-            hipLaunchKernelGGL((linear_prefill_wide_kernel<B, MODE>), dim3(8 * per_xcd), dim3(256), 0, s, m, x,
-                               static_cast<int>(M), y, bias, mblocks, nblocks, jobs, per_xcd);
-        }
-    } else if ((MODE != kModeRaw || EBK_PREFILL_RAW) && xvec && offsets32) {
-        if constexpr (MODE != kModeRaw || EBK_PREFILL_RAW) {
-            const int cus = device_cu_count();
-            if (narrow_workgroups(M, m.rows, 4, cus) <= cus / 2) {
-                launch_narrow<B, MODE, 2>(m, x, M, y, bias, s, cus);
-            } else {
-                launch_narrow<B, MODE, 4>(m, x, M, y, bias, s, cus);
-            }
+        if (prefill_eight_waves<B, MODE>()) return launch_prefill_pp(m, MODE, x, M, y, bias, s);
+        const int mblocks = static_cast<int>((M + kWRows - 1) / kWRows);
+        const int nblocks = (m.rows + kWN - 1) / kWN;
+        const int jobs = mblocks * nblocks;
+        const int per_xcd = (jobs + 7) / 8;
+        hipLaunchKernelGGL((linear_prefill_wide_kernel<B, MODE>), dim3(8 * per_xcd), dim3(256), 0, s, m, x,
+                           static_cast<int>(M), y, bias, mblocks, nblocks, jobs, per_xcd);
+    } else if (xvec && offsets32) {
+        const int cus = device_cu_count();
+        if (narrow_workgroups(M, m.rows, 4, cus) <= cus / 2) {
+            launch_narrow<B, MODE, 2>(m, x, M, y, bias, s, cus);
+        } else {
+            launch_narrow<B, MODE, 4>(m, x, M, y, bias, s, cus);
         }
     } else {
         const dim3 grid((m.rows + kBN - 1) / kBN, static_cast<unsigned>((M + kBM - 1) / kBM));

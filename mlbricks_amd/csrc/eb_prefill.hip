@@ -1,0 +1,373 @@
+// Prefill GEMM on 256 x 256 output tiles with eight waves, two per SIMD.
+//
+// y[M][rows] = x[M][cols] . W^T (+ bias) for M >= 256, W in the bit-plane
+// layout of eb_internal.h, decoded in registers into the B operands of
+// v_mfma_f32_32x32x16_f16; activations go global -> LDS directly.
+//
+// Why two waves per SIMD.  With one wave per SIMD (256 accumulators per
+// lane), counters on configs[3] (14336 x 4096, M = 2048, b = 10) showed the
+// matrix cores busy 47% of the cycles and the waves waiting on memory or
+// LDS results 47% of theirs: nothing else could issue while the only wave
+// of a SIMD waited.  Here wave w owns weight rows 64 (w % 4) .. + 63 (two
+// 32-row blocks) for activation rows 128 (w / 4) .. + 127 (four 32-row
+// blocks): 4 x 2 blocks of 32 x 32, 128 accumulator registers per lane, so
+// two waves fit a SIMD and one multiplies while the other waits.  The two
+// waves of a column group load and decode the same weight bits (the second
+// load hits the CU's L1); the activation reads from LDS are as many as with
+// four waves, since each wave reads only its own 128 rows.
+//
+// Per K step (128 columns = one plane tile) the CU moves 64 KB of
+// activations global -> LDS and 2 x 40 KB (b = 10) of weight bits global ->
+// registers for 512 MFMAs.
+//
+// Pipeline, in half steps h (64 columns: group pair h % 2 of step h / 2):
+//  * activations of half step h go to LDS half-stage h % 4 (32 KB; rows of
+//    128 B whose 16-byte chunks are XOR-swizzled by (row >> 1) & 7, so the
+//    rows read by one operand read land on distinct banks); half step h + 2
+//    is loaded during half step h, one 1 KB load per wave and slice;
+//  * weight bits sit in a register ring of D half steps: with D = 3 (b <= 12)
+//    those of h + 2 are loaded in slices 0 and 1 of half step h; with D = 2
+//    (b >= 13 and raw fp16, whose groups are larger) those of h + 1, in
+//    slice 0, ahead of that slice's activation load;
+//  * a slice (16 columns) is two halves of four MFMAs; the A operands of one
+//    half are read from LDS and the B operands of the next slice decoded
+//    while the other half's MFMAs run;
+//  * one workgroup barrier per half step, before the last slice's second
+//    half: every read of the half-stage being retired has returned and the
+//    next half step's activations and weight bits have landed.
+// Vector loads retire in issue order, so each wait is a count of the loads
+// issued after the ones it needs.  Loads past the last step re-read the
+// last step (clamped addresses), which keeps every count uniform.
+//
+// Launch: workgroup i runs on XCD i % 8, so each XCD walks a contiguous
+// range of tiles, four activation blocks at a time, and the workgroups it
+// runs at once share their activation and weight blocks in its L2.
+#include "eb_device.h"
+
+#include <type_traits>
+
+namespace ebk {
+namespace {
+
+constexpr int kQRows = 256;                  // activation rows per workgroup
+constexpr int kQN = 256;                     // weight rows per workgroup
+constexpr int kQHalfRow = kPRow / 2;         // bytes per staged row of a half step
+constexpr int kQHalf = kQRows * kQHalfRow;   // bytes per half-stage (32 KB)
+constexpr int kQStages = 4;                  // half-stages in the ring
+constexpr int kQCPitch = 2 * kQN + 16;       // bytes per staged output row
+constexpr int kQLds = kQStages * kQHalf > kQRows * kQCPitch ? kQStages * kQHalf : kQRows * kQCPitch;
+constexpr int kQGroupM = 4;                  // activation blocks per tile-order group
+constexpr int kQWaves = 8;
+
+// Depth of the weight-bit register ring (see the pipeline above).
+template <int B, int MODE>
+constexpr int ring_depth() {
+    return (MODE == kModeRaw || B > 12) ? 2 : 3;
+}
+
+template <int B, int MODE>
+__global__ __launch_bounds__(64 * kQWaves) void linear_prefill_pp_kernel(
+    DevMatrix m, const uint16_t* __restrict__ x, int M, uint16_t* __restrict__ y,
+    const uint16_t* __restrict__ bias, int mblocks, int nblocks, int njobs, int per_xcd) {
+    using Bits = GroupBits<B, MODE>;
+    constexpr int GL = GroupLoads<B, MODE>::value;  // vector loads per group
+    constexpr int D = ring_depth<B, MODE>();
+    __shared__ __attribute__((aligned(16))) uint8_t xs[kQLds];
+
+    const int xcd = blockIdx.x & 7;
+    const int local = blockIdx.x >> 3;
+    const int job = xcd * per_xcd + local;
+    if (local >= per_xcd || job >= njobs) return;
+    const int group = job / (kQGroupM * nblocks);
+    const int within = job - group * kQGroupM * nblocks;
+    const int gm = min(kQGroupM, mblocks - group * kQGroupM);
+    const int mb = group * kQGroupM + within % gm;
+    const int nb = within / gm;
+    const int m0 = mb * kQRows;
+    const int n0 = nb * kQN;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // 0 .. 7
+    const int colg = wave & 3;          // weight rows n0 + 64 colg ..
+    const int mh = wave >> 2;           // activation rows m0 + 128 mh ..
+    const int n32 = lane & 31;
+    const int half = lane >> 5;
+    const int steps = m.spr;
+    const int nw0 = n0 + colg * 64;
+
+    // B slots [j][p]: 32-row block j (row tiles nw0/16 + 2j, +1), group pair
+    // p; lane (n32, half) holds group 2p + half of its row, whose codes
+    // 8q .. 8q + 7 are the operand of slice q.
+    uint32_t slot0[2][2];
+    float s[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int rt = min(nw0 / kTileRows + 2 * j + (n32 >> 4), m.rtiles - 1);
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            slot0[j][p] = static_cast<uint32_t>(rt) * static_cast<uint32_t>(steps * kTileSlots) +
+                          static_cast<uint32_t>(16 * (2 * p + half) + (n32 & 15));
+        }
+        s[j] = 0.0f;
+        if constexpr (MODE == kModeW) {
+            const int row = rt * kTileRows + (n32 & 15);
+            s[j] = row < m.rows ? m.scales[row] : 0.0f;
+        }
+    }
+
+    // A of half step h: wave w fills rows 32w .. 32w + 31 of half-stage
+    // h % 4, eight rows (1 KB) per instruction; lane l writes physical chunk
+    // l % 8 of row l / 8, which holds logical chunk (l % 8) ^ ((row >> 1) & 7).
+    // The launcher guarantees cols % 8 == 0, a 16-byte aligned x and
+    // M * cols * 2 below 4 GiB.
+    int achunk[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) achunk[i] = 8 * ((lane & 7) ^ ((4 * i + (lane >> 4)) & 7));
+    const int arow0 = m0 + wave * 32 + (lane >> 3);
+    const uint8_t* xb = reinterpret_cast<const uint8_t*>(x);
+    auto load_a = [&](int h, int i) {
+        const int k0 = min(h >> 1, steps - 1) * kPK + (h & 1) * (kPK / 2);
+        const uint32_t row = static_cast<uint32_t>(min(arow0 + 8 * i, M - 1));
+        const uint32_t off = 2u * (row * static_cast<uint32_t>(m.cols) +
+                                   static_cast<uint32_t>(min(k0 + achunk[i & 1], m.cols - 8)));
+        __builtin_amdgcn_global_load_lds(
+            xb + off, (lds_void_ptr)(xs + (h & 3) * kQHalf + (wave * 32 + 8 * i) * kQHalfRow), 16, 0, 0);
+    };
+    auto load_b = [&](Bits (&r)[2], int h, int j) {
+        const uint32_t st = static_cast<uint32_t>(min(h >> 1, steps - 1));
+        r[j].load32(m, slot0[j][h & 1] + st * kTileSlots);
+    };
+
+    floatx16 acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    // Operands: A in two halves (hh) of two 32-row blocks, each half single-
+    // buffered; B double-buffered by set.  hh, set and q are constants at
+    // every call, so the arrays stay in registers.
+    half8 pa[2][2], pb[2][2];
+    const int aswz = (n32 >> 1) & 7;
+    auto read_a = [&](int hh, int h, int q) {
+        const int chunk = (4 * half + q) ^ aswz;
+        const uint8_t* base = xs + (h & 3) * kQHalf + (128 * mh + 64 * hh + n32) * kQHalfRow + chunk * 16;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) pa[hh][i] = *reinterpret_cast<const half8*>(base + 32 * i * kQHalfRow);
+    };
+    auto decode_b = [&](int set, int j, int q, const Bits (&r)[2]) { pb[set][j] = r[j].operand(q, s[j]); };
+    auto mfma_half = [&](int hh, int set) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                acc[2 * hh + i][j] =
+                    __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[hh][i], pb[set][j], acc[2 * hh + i][j], 0, 0, 0);
+    };
+
+    // Half step h.  rc: its weight bits; rn: those of h + 1 (decoded at the
+    // end for slice 0 of h + 1); rf: the buffer this half step fills (h + 2
+    // with D = 3; with D = 2 it is rn itself, filled with h + 1).
+    //
+    // Slice q, entered with A-low(q) read and B(q) decoded into set q % 2:
+    //   loads; read A-high(q); wait A-low(q); low MFMAs + decode B(q+1)
+    //   block 0; wait A-high(q); read A-low(q+1); high MFMAs + decode B(q+1)
+    //   block 1.
+    // Slice 3 instead waits for the loads of half step h + 1, passes the
+    // barrier and reads A-low of slice 0 of h + 1; its high MFMAs overlap
+    // both decodes of that slice.
+    auto half_step = [&](const Bits (&rc)[2], const Bits (&rn)[2], Bits (&rf)[2], int h) {
+        const bool more = h + 1 < 2 * steps;
+        auto slice = [&](auto q_c) {
+            constexpr int Q = decltype(q_c)::value;
+            constexpr int SET = Q & 1;
+            if constexpr (D == 3) {
+                load_a(h + 2, Q);
+                if constexpr (Q < 2) load_b(rf, h + 2, Q);
+            } else {
+                if constexpr (Q == 0) {
+                    load_b(rf, h + 1, 0);
+                    load_b(rf, h + 1, 1);
+                }
+                load_a(h + 2, Q);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            read_a(1, h, Q);
+            wait_lgkmcnt<2>();                     // A-low(q) landed
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_half(0, SET);
+            if constexpr (Q < 3) decode_b(SET ^ 1, 0, Q + 1, rc);
+            __builtin_amdgcn_sched_barrier(0);
+            wait_lgkmcnt<0>();                     // A-high(q) landed
+            if constexpr (Q == 3) {
+                // A and B of half step h + 1 landed: younger are this half
+                // step's four activation loads and, with D = 3, its two
+                // weight groups (with D = 2 its weight groups are the ones
+                // waited for, issued before its activation loads)
+                wait_vmcnt<D == 3 ? 4 + 2 * GL : 4>();
+                barrier_after_wait();
+                __builtin_amdgcn_sched_barrier(0);
+                if (more) read_a(0, h + 1, 0);
+            } else {
+                read_a(0, h, Q + 1);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_half(1, SET);
+            if constexpr (Q < 3) {
+                decode_b(SET ^ 1, 1, Q + 1, rc);
+            } else {
+                if (more) {
+                    decode_b(0, 0, 0, rn);
+                    decode_b(0, 1, 0, rn);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        slice(std::integral_constant<int, 0>{});
+        slice(std::integral_constant<int, 1>{});
+        slice(std::integral_constant<int, 2>{});
+        slice(std::integral_constant<int, 3>{});
+    };
+
+    Bits ring0[2], ring1[2], ring2[2];
+    // prologue: A of half steps 0 and 1, weight bits of half step 0 (and 1
+    // with D = 3)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) load_a(0, i);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) load_b(ring0, 0, j);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) load_a(1, i);
+    if constexpr (D == 3) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) load_b(ring1, 1, j);
+    }
+    wait_vmcnt<0>();
+    barrier_after_wait();
+    read_a(0, 0, 0);
+    decode_b(0, 0, 0, ring0);
+    decode_b(0, 1, 0, ring0);
+    if constexpr (D == 3) {
+        // One step (two half steps) per iteration; the ring advances by two
+        // buffers, (r0, r1, r2) <- (r2, r0, r1), by register copies.
+        for (int st = 0; st < steps; ++st) {
+            half_step(ring0, ring1, ring2, 2 * st);
+            half_step(ring1, ring2, ring0, 2 * st + 1);
+            Bits t[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                t[j].copy_from(ring0[j]);
+                ring0[j].copy_from(ring2[j]);
+                ring2[j].copy_from(ring1[j]);
+                ring1[j].copy_from(t[j]);
+            }
+        }
+    } else {
+        (void)ring2;
+        for (int st = 0; st < steps; ++st) {
+            half_step(ring0, ring1, ring1, 2 * st);
+            half_step(ring1, ring0, ring0, 2 * st + 1);
+        }
+    }
+
+    // ---- epilogue: the whole 256 x 256 tile through LDS ----
+    // 32x32 block element e of lane l is D[8*(e/4) + 4*(l/32) + e%4][l%32].
+    // The clamped re-loads of the last step must land before the LDS is
+    // reused.
+    wait_vmcnt<0>();
+    __syncthreads();
+    static_assert(kQRows * kQCPitch <= kQLds, "output staging exceeds the LDS");
+    float sn[2];
+    uint16_t bn[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int n = min(nw0 + 32 * j + n32, m.rows - 1);
+        sn[j] = 1.0f;
+        bn[j] = 0;
+        if constexpr (MODE == kModeQ) sn[j] = m.scales[n];
+        if (bias) bn[j] = bias[n];
+    }
+    {
+        uint8_t* cw = xs + (128 * mh) * kQCPitch + colg * 128;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int r = 32 * i + 8 * (e >> 2) + 4 * half + (e & 3);
+                    *reinterpret_cast<uint16_t*>(cw + r * kQCPitch + (32 * j + n32) * 2) =
+                        epilogue<MODE>(acc[i][j][e], sn[j], bias != nullptr, bn[j]);
+                }
+    }
+    __syncthreads();
+    const bool yvec = (m.rows % 8 == 0) && (reinterpret_cast<uintptr_t>(y) % 16 == 0);
+    const int chunk = threadIdx.x & 31;         // 16-byte chunk of a 512-byte row
+#pragma unroll 4
+    for (int it = 0; it < kQRows / (64 * kQWaves / 32); ++it) {
+        const int r = it * (64 * kQWaves / 32) + (threadIdx.x >> 5);
+        const int gr = m0 + r;
+        const int gn = n0 + chunk * 8;
+        if (gr >= M || gn >= m.rows) continue;
+        const uint4 v = *reinterpret_cast<const uint4*>(xs + r * kQCPitch + chunk * 16);
+        uint16_t* dst = y + static_cast<size_t>(gr) * m.rows + gn;
+        if (yvec) {
+            *reinterpret_cast<uint4*>(dst) = v;
+        } else {
+            const uint16_t* hv = reinterpret_cast<const uint16_t*>(&v);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                if (gn + k < m.rows) dst[k] = hv[k];
+            }
+        }
+    }
+}
+
+template <int B, int MODE>
+hipError_t launch_pp(const DevMatrix& m, const uint16_t* x, int64_t M, uint16_t* y, const uint16_t* bias,
+                     hipStream_t s) {
+    const int mblocks = static_cast<int>((M + kQRows - 1) / kQRows);
+    const int nblocks = (m.rows + kQN - 1) / kQN;
+    const int jobs = mblocks * nblocks;
+    const int per_xcd = (jobs + 7) / 8;
+    hipLaunchKernelGGL((linear_prefill_pp_kernel<B, MODE>), dim3(8 * per_xcd), dim3(64 * kQWaves), 0, s, m, x,
+                       static_cast<int>(M), y, bias, mblocks, nblocks, jobs, per_xcd);
+    return hipGetLastError();
+}
+
+template <int B>
+hipError_t launch_pp_bits(const DevMatrix& m, int mode, const uint16_t* x, int64_t M, uint16_t* y,
+                          const uint16_t* bias, hipStream_t s) {
+    if constexpr (B <= 12) {
+        if (mode == kModeQ) return launch_pp<B, kModeQ>(m, x, M, y, bias, s);
+    }
+    if (mode == kModeW) return launch_pp<B, kModeW>(m, x, M, y, bias, s);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+hipError_t launch_prefill_pp(const DevMatrix& m, int mode, const uint16_t* x, int64_t M, uint16_t* y,
+                             const uint16_t* bias, hipStream_t s) {
+    if (mode == kModeRaw) return launch_pp<8, kModeRaw>(m, x, M, y, bias, s);
+    switch (m.bits) {
+        case 3: return launch_pp_bits<3>(m, mode, x, M, y, bias, s);
+        case 4: return launch_pp_bits<4>(m, mode, x, M, y, bias, s);
+        case 5: return launch_pp_bits<5>(m, mode, x, M, y, bias, s);
+        case 6: return launch_pp_bits<6>(m, mode, x, M, y, bias, s);
+        case 7: return launch_pp_bits<7>(m, mode, x, M, y, bias, s);
+        case 8: return launch_pp_bits<8>(m, mode, x, M, y, bias, s);
+        case 9: return launch_pp_bits<9>(m, mode, x, M, y, bias, s);
+        case 10: return launch_pp_bits<10>(m, mode, x, M, y, bias, s);
+        case 11: return launch_pp_bits<11>(m, mode, x, M, y, bias, s);
+        case 12: return launch_pp_bits<12>(m, mode, x, M, y, bias, s);
+        case 13: return launch_pp_bits<13>(m, mode, x, M, y, bias, s);
+        case 14: return launch_pp_bits<14>(m, mode, x, M, y, bias, s);
+        case 15: return launch_pp_bits<15>(m, mode, x, M, y, bias, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace ebk

@@ -215,7 +215,7 @@ def test_forward_ragged_shapes(native, b, rows, cols, M):
 
 @pytest.mark.parametrize("rows,cols,M", [(7, 13, 40), (33, 65, 40), (5, 1000, 40), (300, 1000, 513),
                                          (520, 1000, 300), (100, 2056, 64)])
-@pytest.mark.parametrize("tiles", ["auto", "wide"])
+@pytest.mark.parametrize("tiles", ["auto", "wide", "wide8"])
 def test_fp16_fallback_prefill_ragged(native, rows, cols, M, tiles):
     """b = 16 (raw fp16 weights) through the prefill kernels: K not a whole
     number of 32-column groups (the padded tail of the last group must
@@ -462,12 +462,17 @@ def test_config2_decode_gemv_4096(native, M):
     assert _rel_max(y, full) <= TOL
 
 
-def test_config4_prefill_gemm_14336(native):
+@pytest.mark.parametrize("tiles", ["auto", "wide", "wide8"])
+def test_config4_prefill_gemm_14336(native, tiles):
     rows, cols, b, M = 14336, 4096, 10, 2048
     m, payload, s = _config_matrix(native, rows, cols, b)
     x = torch.randn(M, cols, generator=torch.Generator().manual_seed(1)).half().cuda()
-    y = m.forwardTorch(x)
-    torch.cuda.synchronize()
+    native.set_prefill_tiles(tiles)
+    try:
+        y = m.forwardTorch(x)
+        torch.cuda.synchronize()
+    finally:
+        native.set_prefill_tiles("auto")
     sub = 16
     ref = ora.linear_intdot(payload[: sub * cols * b // 8], s[:sub], sub, cols, b,
                             x[:256].cpu().numpy().view(np.uint16))
@@ -548,11 +553,11 @@ def test_legacy_packed_linear_dtypes_and_torch_op(native, dtype):
 # shapes hit: only half tiles (108 tiles), only whole tiles (204), and a mix
 # (308 = 256 whole + 52 split), each with a partial K step, in both the
 # integer-dot and the decoded-fp16 arithmetic.
-@pytest.fixture
-def wide_tiles(native):
-    """Force the 256 x 256 prefill tiles for one test (the automatic choice
-    takes them only for large grids)."""
-    native.set_prefill_tiles("wide")
+@pytest.fixture(params=["wide", "wide8"])
+def wide_tiles(native, request):
+    """Force the 256 x 256 prefill tiles, with four and with eight waves, for
+    one test (the automatic choice takes them only for large grids)."""
+    native.set_prefill_tiles(request.param)
     yield
     native.set_prefill_tiles("auto")
 
