@@ -8,7 +8,7 @@
 // q_b = clamp(rint(w / s_b), -qmax_b, qmax_b) (core.py:151-153):
 //   ref    = fp16(x . W^T)                           (core.py:140)
 //   full_b = fp16(x . fp16(q_b * s_b)^T)             (core.py:154-158)
-//   hw_b   = fp16(fp32(x . q_b^T) * s_b), b <= 8     (core.py:160-169)
+//   hw_b   = fp16(fp32(x . q_b^T) * s_b), b <= 12    (core.py:160-169)
 // and the squared distances |full_b - ref|^2, |hw_b - ref|^2 and |ref|^2,
 // summed per tile of 16 weight rows.  The caller adds the tiles and forms
 // relL2 = sqrt(sum |c - ref|^2) / max(sqrt(sum |ref|^2), 1e-30)
@@ -16,8 +16,14 @@
 //
 // Products run on v_mfma_f32_16x16x32_f16 with fp32 accumulation, as the
 // vendor GEMM does; every fp16 operand is exact (fp16(q*s) is the decoded
-// weight, and |q| <= 127 is an fp16 integer for the b <= 8 codes).  The
+// weight, and |q| <= 2047 is an fp16 integer for the b <= 12 codes).  The
 // division w / s_b is IEEE fp32 (no fast-math), as torch's.
+//
+// The reference measures hw_b only for b <= 8: above that its
+// hardwareNative policy executes W16A16, whose output is full_b.  This
+// runtime's hardwareNative executes the integer-code product up to b = 12
+// (the codes stay exact fp16 integers), so hw_b is measured up to b = 12
+// and the width search checks the arithmetic that will run.
 #include "eb_internal.h"
 
 #include <hip/hip_runtime.h>
@@ -33,7 +39,7 @@ constexpr int kAnWaves = 4;                   // waves split the 32-column chunk
 constexpr int kAnBlocks = kAnalyzeMaxSamples / 16;   // 16-row calibration blocks (MFMA m)
 constexpr int kLo = 3;                        // widths kLo .. kLo + kWidths - 1
 constexpr int kWidths = 13;
-constexpr int kHw = 6;                        // b = 3..8 also run the integer-code product
+constexpr int kHw = 10;                       // b = 3..12 also run the integer-code product
 constexpr int kSets = 1 + kWidths + kHw;      // ref, full_b, hw_b
 static_assert(kSets == kAnalyzeSums, "partial sums per tile");
 
@@ -164,7 +170,7 @@ __global__ __launch_bounds__(64 * kAnWaves) void analyze_widths_kernel(
         }
     }
 
-    // Workgroup sums of the 20 sets, in a fixed order: lanes by a shuffle
+    // Workgroup sums of the kSets sets, in a fixed order: lanes by a shuffle
     // tree, then the waves through LDS.
     __shared__ float wsum[kAnWaves][kSets];
 #pragma unroll

@@ -201,7 +201,7 @@ def backendInfo() -> dict:
     }
 
 
-PREFILL_TILES = {"auto": 0, "narrow": 1, "wide": 2}
+PREFILL_TILES = {"auto": 0, "narrow": 1, "wide": 2, "wide8": 3}
 
 
 def forward_torch_multi(matrices: Sequence["RuntimeMatrix"], input: torch.Tensor,
@@ -246,7 +246,7 @@ def forward_torch_multi(matrices: Sequence["RuntimeMatrix"], input: torch.Tensor
 
 ANALYZE_TILE_ROWS = 16
 ANALYZE_MAX_SAMPLES = 32
-ANALYZE_SUMS = 20
+ANALYZE_SUMS = 24
 ANALYZE_WIDTHS = tuple(range(3, 16))
 
 
@@ -256,8 +256,9 @@ def width_errors_torch(weight: torch.Tensor, calibration16: torch.Tensor) -> tup
     ``[samples, cols]`` on the same device, from one fused pass over the
     weights (eb_analyze_widths_device; the measurement of _selectBitsTorch,
     core.py:112-195).  Returns ``(full, hw)``, float64 arrays indexed by
-    b - 3; ``hw`` equals ``full`` for b >= 9, where hardwareNative runs W16A16
-    (core.py:170-172)."""
+    b - 3.  ``hw`` is the integer-code output's error for b <= 12 (the
+    arithmetic hardwareNative runs there) and equals ``full`` for b >= 13,
+    where hardwareNative runs W16A16."""
     if not weight.is_cuda or weight.dtype != torch.float16 or weight.dim() != 2:
         raise ValueError("width search needs fp16 CUDA weights [rows, cols]")
     if calibration16.device != weight.device or calibration16.dtype != torch.float16 or \
@@ -283,15 +284,16 @@ def width_errors_torch(weight: torch.Tensor, calibration16: torch.Tensor) -> tup
     den = max(float(np.sqrt(sums[0])), 1.0e-30)
     full = np.sqrt(sums[1:14]) / den
     hw = full.copy()
-    hw[:6] = np.sqrt(sums[14:20]) / den
+    hw[:10] = np.sqrt(sums[14:24]) / den
     return full, hw
 
 
 def set_prefill_tiles(mode: str) -> None:
     """Tile shape of the prefill route (M > 16, b <= 15): 'auto' (default,
-    picked by estimated rounds over the compute units), 'narrow' (128 x 256)
-    or 'wide' (256 x 256).  Process-wide; a tuning and test control with no
-    counterpart in the reference."""
+    picked by estimated rounds over the compute units), 'narrow' (128 x 256),
+    'wide' (256 x 256, four waves) or 'wide8' (256 x 256, eight waves).
+    Process-wide; a tuning and test control with no counterpart in the
+    reference."""
     if mode not in PREFILL_TILES:
         raise ValueError(f"prefill tile mode must be one of {sorted(PREFILL_TILES)}")
     check(_lib.eb_set_prefill_tiles(PREFILL_TILES[mode]))
