@@ -1,36 +1,38 @@
-"""ElasticBit adaptive threshold-driven weight compression on MI355X.
+"""ElasticBit: threshold-driven weight compression with a HIP execution path.
 
-Public contract (same as ``mlbricks/elasticbit/core.py``): the user supplies
-calibration data and an error threshold; ElasticBit picks the smallest storage
-width b in 3..15 whose hardware-native and full-precision outputs both stay
-within the threshold, with fp16 (b = 16) as the fallback.  Storage is the
-canonical MLB4 bitstream with one fp32 scale per row.
+The public contract is that of ``mlbricks/elasticbit/core.py``.  Given
+calibration inputs and an error threshold, each ``nn.Linear`` gets the smallest
+storage width b in 3..15 whose outputs stay within the threshold, else fp16
+(b = 16).  Storage is the canonical MLB4 bitstream with one fp32 scale per
+output row.  Names, signatures, error messages and the ``.elasticbit`` zip
+layout are kept so that the module drops in; the implementation is this
+package's own.
 
-Execution on gfx950 reads the b-bit codes directly -- re-laid out at load time
-as bit planes, still b bits per weight -- and decodes them in registers:
+Execution on gfx950 keeps the b-bit codes on the device (re-laid out as bit
+planes, still b bits per weight) and decodes them in registers:
 
-* ``hardwareNative``: b <= 12 multiplies the exact integer codes (every
-  |q| <= 2047 is an fp16 integer) by fp16 activations and applies the row
-  scale once; b >= 13 uses the decoded fp16 weights fp16_rn(q*s) (W16A16
-  arithmetic, as the reference does for b >= 9);
-* ``fullPrecision``: every width uses the decoded fp16 weights;
-* one fused kernel family serves decode (M <= 16, and up to 64 where it is
-  faster) and prefill on the matrix cores; activations stay fp16 everywhere.
+* ``hardwareNative``: for b <= 12 the exact integer codes (every |q| <= 2047
+  is an fp16 integer) multiply the fp16 activations and the row scale is
+  applied once; b >= 13 uses the decoded weights fp16_rn(q*s);
+* ``fullPrecision``: the decoded weights at every width.
 
-``_ElasticLinear`` routes through the execution planner: ``backend='auto'``
-qualifies the HIP route against the PyTorch route (materialize + F.linear)
-once per phase and freezes the winner.
+``_ElasticLinear`` routes each call through the execution planner.  Under
+``backend='auto'`` it qualifies the HIP route against the PyTorch route, once
+per phase, and freezes the winner.  The PyTorch route is what the reference
+executes: ``F.linear`` on a resident fp16 copy of the weights for b >= 9,
+and on a copy materialized per call for b <= 8.
 """
 from __future__ import annotations
 
 import gc
+import io
 import json
 import os
 import tempfile
 import zipfile
-from dataclasses import dataclass
+from dataclasses import dataclass, fields
 from pathlib import Path
-from typing import Any, Mapping, Sequence
+from typing import Any, Callable, Iterable, Mapping, Sequence
 
 import numpy as np
 import torch
@@ -43,40 +45,43 @@ from .native_api import available as _nativeAvailable
 from .native_api import importError as _nativeImportError
 from .native_api import requireNative as _requireNative
 
-_VALID_POLICIES = {"hardwareNative", "fullPrecision"}
-_MODEL_FORMAT = "ElasticBitModel"
-_MODEL_FORMAT_VERSION = 1
-# Linear calls with at most this many activation rows qualify as "decode":
-# the native route runs its decode kernel up to 64 rows, where it reads the
-# weights once and leads the materialize + F.linear route by 3-4x, so a
-# batched decode is not tied to the route a long prompt chose.
-_DECODE_MAX_ROWS = 64
+DECODE_POLICIES = ("hardwareNative", "fullPrecision")
+ARTIFACT_FORMAT = ("ElasticBitModel", 1)          # manifest "format", "version"
+CALIBRATION_ROWS = 32                             # kept per Linear (core.py:734)
+# Calls with at most this many activation rows are the "decode" phase: the
+# native route runs its decode kernel up to 64 rows, so a batched decode is
+# qualified apart from a long prompt.
+DECODE_PHASE_ROWS = 64
+_RESIDENT_MIN_BITS = 9                            # the reference keeps fp16 resident from here
 
+
+# -- argument coercion ----------------------------------------------------------
 
 def _checkPolicy(value: str) -> str:
-    value = str(value)
-    if value not in _VALID_POLICIES:
-        raise ValueError("decodePolicy must be 'hardwareNative' or 'fullPrecision'")
-    return value
+    policy = str(value)
+    if policy in DECODE_POLICIES:
+        return policy
+    raise ValueError("decodePolicy must be 'hardwareNative' or 'fullPrecision'")
 
 
-def _toNumpy2D(value: Any, *, name: str) -> np.ndarray:
-    if torch.is_tensor(value):
-        value = value.detach().float().cpu().numpy()
-    array = np.asarray(value, dtype=np.float32)
+def _matrix_f32(value: Any, name: str) -> np.ndarray:
+    """A C-contiguous float32 2-D copy of a tensor or array-like."""
+    host = value.detach().to("cpu", torch.float32).numpy() if torch.is_tensor(value) else value
+    array = np.ascontiguousarray(host, dtype=np.float32)
     if array.ndim != 2:
         raise ValueError(f"{name} must be a 2D matrix")
-    return np.ascontiguousarray(array, dtype=np.float32)
+    return array
 
 
-def _toCalibrationBatches(calibrationData: Any) -> list[Any]:
-    """core.py:71-82: one batch, a mapping, or an iterable of batches."""
+def _batch_list(calibrationData: Any) -> list[Any]:
+    """Calibration as a list of model inputs (core.py:71-82): one tensor or
+    mapping is a single batch; any other iterable is a sequence of batches."""
     if torch.is_tensor(calibrationData) or isinstance(calibrationData, Mapping):
         return [calibrationData]
     if isinstance(calibrationData, (str, bytes)):
         raise TypeError("calibrationData must contain model inputs, not text")
     try:
-        batches = list(calibrationData)
+        batches = [batch for batch in calibrationData]
     except TypeError as exc:
         raise TypeError("calibrationData must be a model input or an iterable of model inputs") from exc
     if not batches:
@@ -84,25 +89,44 @@ def _toCalibrationBatches(calibrationData: Any) -> list[Any]:
     return batches
 
 
-def _callModel(model: nn.Module, batch: Any) -> Any:
-    if isinstance(batch, Mapping):
-        return model(**batch)
-    if isinstance(batch, tuple):
-        return model(*batch)
-    return model(batch)
-
-
-def _moveBatch(batch: Any, device: torch.device) -> Any:
+def _on_device(batch: Any, device: torch.device) -> Any:
     if torch.is_tensor(batch):
         return batch.to(device)
     if isinstance(batch, Mapping):
-        return {k: _moveBatch(v, device) for k, v in batch.items()}
-    if isinstance(batch, tuple):
-        return tuple(_moveBatch(v, device) for v in batch)
-    if isinstance(batch, list):
-        return [_moveBatch(v, device) for v in batch]
+        return {key: _on_device(item, device) for key, item in batch.items()}
+    if isinstance(batch, (tuple, list)):
+        return type(batch)(_on_device(item, device) for item in batch)
     return batch
 
+
+def _feed(model: nn.Module, batch: Any) -> None:
+    """Run one calibration batch: keyword inputs, positional inputs, or one input."""
+    if isinstance(batch, Mapping):
+        model(**batch)
+    elif isinstance(batch, tuple):
+        model(*batch)
+    else:
+        model(batch)
+
+
+def _device_of(module: nn.Module) -> torch.device:
+    tensor = next(iter(module.parameters()), None)
+    if tensor is None:
+        tensor = next(iter(module.buffers()), None)
+    return torch.device("cpu") if tensor is None else tensor.device
+
+
+def _replaceNamedModule(root: nn.Module, name: str, replacement: nn.Module) -> None:
+    """Swap the submodule at dotted path ``name``; the root itself cannot be
+    replaced (core.py:206-213)."""
+    if not name:
+        raise ValueError("ElasticBit cannot replace the root module")
+    parent_name, _, leaf = name.rpartition(".")
+    parent = root.get_submodule(parent_name) if parent_name else root
+    parent._modules[leaf] = replacement
+
+
+# -- GPU width selection --------------------------------------------------------
 
 @torch.inference_mode()
 def _selectBitsTorch(weight: torch.Tensor, calibration: np.ndarray, threshold: float,
@@ -110,16 +134,17 @@ def _selectBitsTorch(weight: torch.Tensor, calibration: np.ndarray, threshold: f
                      ) -> tuple[int, float, np.ndarray | torch.Tensor | None, np.ndarray | None]:
     """Width selection on the model's GPU (core.py:112-195).
 
-    For b = 3..15: s = max|w_r| / qmax (1 for a zero row), q = clamp(round(w/s)),
-    full = F.linear(x16, fp16(q*s)), and for b <= 8 also
-    hw = fp16((x16.float() @ q^T) * s); the first b with
-    max(relL2(ref, hw), relL2(ref, full)) <= threshold wins, ref = F.linear(x16, W16).
-    The errors of all thirteen widths come from one fused HIP pass over the
-    weights (``width_errors_torch``); only the selected width is quantized
-    here, and its codes and scales are returned so packing never
-    re-quantizes.  ``codesOnDevice`` keeps the codes as an int16 tensor on
-    the weight's device (for ``_compressSelectedCodesTorch``) instead of a
-    numpy copy.
+    The reference's rule: for b = 3..15, s = max|w_r| / qmax (1 for a zero
+    row), q = clamp(round(w/s)), full = F.linear(x16, fp16(q*s)) and, for
+    b <= 8, hw = fp16((x16.float() @ q^T) * s); the first b whose
+    max(relL2(ref, hw), relL2(ref, full)) <= threshold wins, with
+    ref = F.linear(x16, W16).  Here one fused HIP pass
+    (``width_errors_torch``) yields the errors of all thirteen widths; the
+    hw error is the integer-code output's at every b <= 12, because that is
+    the arithmetic the HIP route runs there.  Only the chosen width is then
+    quantized, and its codes and scales are returned so that packing never
+    quantizes again.  ``codesOnDevice`` leaves the codes as an int16 tensor
+    on the weight's device.
     """
     if weight.device.type != "cuda":
         raise RuntimeError("ElasticBit GPU analyzer requires CUDA weights")
@@ -128,50 +153,34 @@ def _selectBitsTorch(weight: torch.Tensor, calibration: np.ndarray, threshold: f
     if not np.isfinite(threshold) or float(threshold) < 0.0:
         raise ValueError("threshold must be a finite non-negative value")
     native = _requireNative()
-    x16 = torch.from_numpy(np.ascontiguousarray(calibration, dtype=np.float32)).to(
-        device=weight.device, dtype=torch.float16)
+    x16 = torch.as_tensor(np.ascontiguousarray(calibration, dtype=np.float32)).to(weight.device, torch.float16)
     w = weight.detach()
     full, hw = native.width_errors_torch(w, x16)
-    for bits in range(3, 16):
-        err = max(float(hw[bits - 3]), float(full[bits - 3]))
-        if err <= float(threshold):
-            codes, scales = _quantizeRowsTorch(w, bits)
-            if not codesOnDevice:
-                codes = np.ascontiguousarray(codes.cpu().numpy(), dtype=np.int16)
-            return bits, err, codes, scales
-    return 16, 0.0, None, None
+    errors = np.maximum(np.asarray(full, np.float64), np.asarray(hw, np.float64))
+    passing = np.flatnonzero(errors <= float(threshold))
+    if passing.size == 0:
+        return 16, 0.0, None, None
+    bits = int(passing[0]) + 3
+    codes, scales = _quantizeRowsTorch(w, bits)
+    if not codesOnDevice:
+        codes = np.ascontiguousarray(codes.cpu().numpy(), dtype=np.int16)
+    return bits, float(errors[bits - 3]), codes, scales
 
 
 def _quantizeRowsTorch(weight: torch.Tensor, bits: int) -> tuple[torch.Tensor, np.ndarray]:
-    """Codes (int16, on the weight's device) and row scales of one width, as
-    core.py:142-155 forms them."""
+    """Codes (int16, on the weight's device) and row scales of one width, with
+    the reference's torch expressions (core.py:142-155): the scale divides a
+    tensor by a Python scalar, which torch's kernels compute as a product
+    with fp32(1/qmax)."""
     w32 = weight.float()
-    max_abs = w32.abs().amax(dim=1)
+    peak = w32.abs().amax(dim=1)
     qmax = float((1 << (bits - 1)) - 1)
-    scale = torch.where(max_abs > 0.0, max_abs / qmax, torch.ones_like(max_abs))
-    q = torch.round(w32 / scale[:, None]).clamp(min=-qmax, max=qmax)
-    codes = q.to(torch.int16).contiguous()
-    scales = np.ascontiguousarray(scale.float().cpu().numpy(), dtype=np.float32)
-    return codes, scales
+    scale = torch.where(peak > 0.0, peak / qmax, torch.ones_like(peak))
+    codes = torch.round(w32 / scale[:, None]).clamp(min=-qmax, max=qmax).to(torch.int16).contiguous()
+    return codes, np.ascontiguousarray(scale.cpu().numpy(), dtype=np.float32)
 
 
-def _moduleDevice(module: nn.Module) -> torch.device:
-    for p in module.parameters():
-        return p.device
-    for b in module.buffers():
-        return b.device
-    return torch.device("cpu")
-
-
-def _replaceNamedModule(root: nn.Module, name: str, replacement: nn.Module) -> None:
-    parts = name.split(".") if name else []
-    if not parts:
-        raise ValueError("ElasticBit cannot replace the root module")
-    parent = root
-    for part in parts[:-1]:
-        parent = parent._modules[part]
-    parent._modules[parts[-1]] = replacement
-
+# -- result records (field names are the public interface) -----------------------
 
 @dataclass(frozen=True)
 class BitCandidate:
@@ -208,112 +217,138 @@ class BackendInfo:
     decodeStatus: str | None = None
     decodeValidation: str | None = None
 
+    _SHOWN = ("device", "architecture", "weightWidths", "activateDType", "prefill", "decodePlanner",
+              "decodeEngine", "decodeStatus", "decodeValidation")
+
     def __str__(self) -> str:
         if not self.available:
             return f"ElasticBitBackend(unavailable, error={self.error!r})"
-        return ("ElasticBitBackend("
-                f"device={self.device!r}, architecture={self.architecture!r}, "
-                f"weightWidths={self.weightWidths}, activateDType={self.activateDType!r}, "
-                f"prefill={self.prefill!r}, decodePlanner={self.decodePlanner!r}, "
-                f"decodeEngine={self.decodeEngine!r}, decodeStatus={self.decodeStatus!r}, "
-                f"decodeValidation={self.decodeValidation!r}, validated={self.validated})")
+        parts = [f"{name}={getattr(self, name)!r}" for name in self._SHOWN]
+        parts[2] = f"weightWidths={self.weightWidths}"
+        return "ElasticBitBackend(" + ", ".join(parts + [f"validated={self.validated}"]) + ")"
+
+
+def _unavailable_backend(error: str | None, widths: Iterable[int] = (), dtype: str | None = None) -> BackendInfo:
+    return BackendInfo(available=False, device=None, deviceIndex=None, architecture=None,
+                       weightWidths=tuple(widths), activateDType=dtype, prefill=None, decodePlanner=None,
+                       validated=False, error=error)
+
+
+# -- the single-matrix handle ----------------------------------------------------
+
+def _native_reader(name: str, cast: Callable[[Any], Any]) -> property:
+    return property(lambda self: cast(getattr(self._native, name)), doc=f"The matrix's {name}.")
 
 
 class RuntimeMatrix:
-    """Single-matrix ElasticBit runtime (core.py:264-424).
+    """One ElasticBit matrix on the HIP runtime (core.py:264-424).
 
-    Built only by :meth:`compress` and :meth:`load`; there is no constructor
-    that takes a user-chosen bit width."""
+    Built only by :meth:`compress`, :meth:`load` and the analyzer-driven
+    internal factories; no constructor takes a user-chosen bit width."""
 
     def __init__(self, native: Any) -> None:
         self._native = native
+        self._resident: torch.Tensor | None = None
+
+    # factories ------------------------------------------------------------
+
+    @classmethod
+    def _build(cls, factory: str, *args: Any) -> "RuntimeMatrix":
+        native = _requireNative()
+        return cls(getattr(native.RuntimeMatrix, factory)(*args))
 
     @classmethod
     def compress(cls, weights: Any, calibrationData: Any, threshold: float,
                  decodePolicy: str = "hardwareNative") -> "RuntimeMatrix":
-        native = _requireNative()
+        _requireNative()
         policy = _checkPolicy(decodePolicy)
-        w = _toNumpy2D(weights, name="weights")
-        c = _toNumpy2D(calibrationData, name="calibrationData")
-        return cls(native.RuntimeMatrix.compress(w, c, float(threshold), policy))
+        return cls._build("compress", _matrix_f32(weights, "weights"), _matrix_f32(calibrationData, "calibrationData"),
+                          float(threshold), policy)
 
     @classmethod
     def _compressSelected(cls, weights: Any, selectedBits: int, threshold: float, selectedError: float,
                           decodePolicy: str = "hardwareNative") -> "RuntimeMatrix":
-        native = _requireNative()
+        _requireNative()
         policy = _checkPolicy(decodePolicy)
-        w = _toNumpy2D(weights, name="weights")
-        return cls(native.RuntimeMatrix._compressSelected(w, int(selectedBits), float(threshold),
-                                                          float(selectedError), policy))
+        return cls._build("_compressSelected", _matrix_f32(weights, "weights"), int(selectedBits), float(threshold),
+                          float(selectedError), policy)
 
     @classmethod
     def _compressSelectedCodes(cls, codes: np.ndarray, scales: np.ndarray, selectedBits: int,
                                threshold: float, selectedError: float,
                                decodePolicy: str = "hardwareNative") -> "RuntimeMatrix":
-        """Pack an analyzer result as selected, without re-quantizing."""
-        native = _requireNative()
+        """Pack an analyzer result as selected, without quantizing again."""
+        _requireNative()
         policy = _checkPolicy(decodePolicy)
         q = np.ascontiguousarray(codes, dtype=np.int16)
         s = np.ascontiguousarray(scales, dtype=np.float32)
         if q.ndim != 2:
             raise ValueError("codes must be a 2D matrix")
-        if s.ndim != 1 or s.shape[0] != q.shape[0]:
+        if s.shape != (q.shape[0],):
             raise ValueError("scales must contain one value per weight row")
-        return cls(native.RuntimeMatrix._compressSelectedCodes(q, s, int(selectedBits), float(threshold),
-                                                               float(selectedError), policy))
+        return cls._build("_compressSelectedCodes", q, s, int(selectedBits), float(threshold), float(selectedError),
+                          policy)
 
     @classmethod
     def _compressSelectedCodesTorch(cls, codes: torch.Tensor, scales: np.ndarray, selectedBits: int,
                                     threshold: float, selectedError: float,
                                     decodePolicy: str = "hardwareNative") -> "RuntimeMatrix":
-        """_compressSelectedCodes for codes that are an int16 tensor on the
-        HIP device: packed on the device, without a host copy of the codes."""
-        native = _requireNative()
+        """``_compressSelectedCodes`` for int16 codes already on the HIP
+        device: packed there, with no host copy of the codes."""
+        _requireNative()
         policy = _checkPolicy(decodePolicy)
-        return cls(native.RuntimeMatrix._compressSelectedCodesTorch(codes, scales, int(selectedBits),
-                                                                    float(threshold), float(selectedError), policy))
+        return cls._build("_compressSelectedCodesTorch", codes, scales, int(selectedBits), float(threshold),
+                          float(selectedError), policy)
 
     @classmethod
     def load(cls, path: str | Path, decodePolicy: str = "hardwareNative") -> "RuntimeMatrix":
-        native = _requireNative()
-        policy = _checkPolicy(decodePolicy)
-        return cls(native.RuntimeMatrix.load(str(path), policy))
+        _requireNative()
+        return cls._build("load", str(path), _checkPolicy(decodePolicy))
+
+    # execution ------------------------------------------------------------
 
     def forward(self, x: Any) -> Any:
-        """GPU fp16 activations stay on the device (any number of rows);
-        anything else takes the host round trip of one row."""
-        if torch.is_tensor(x):
-            if x.is_cuda and x.dtype == torch.float16 and x.dim() >= 1 and x.shape[-1] == self.cols:
-                return self._native.forwardTorch(x.contiguous())
-            values = np.asarray(x.detach().float().cpu().numpy(), dtype=np.float32).reshape(-1)
-            out = self._native.forward(np.ascontiguousarray(values))
-            return torch.from_numpy(np.asarray(out)).to(device=x.device, dtype=x.dtype)
-        values = np.asarray(x, dtype=np.float32).reshape(-1)
-        return np.asarray(self._native.forward(np.ascontiguousarray(values)))
+        """fp16 activations on the matrix's device stay there (any number of
+        rows ``[..., cols]``); anything else makes the host round trip of one
+        row, as the reference's numpy path does."""
+        if torch.is_tensor(x) and x.is_cuda and x.dtype == torch.float16 and x.dim() >= 1 \
+                and x.shape[-1] == self.cols:
+            return self._native.forwardTorch(x.contiguous())
+        host = x.detach().to("cpu", torch.float32).numpy() if torch.is_tensor(x) else x
+        row = np.ascontiguousarray(np.asarray(host, dtype=np.float32).reshape(-1))
+        out = np.asarray(self._native.forward(row))
+        return torch.from_numpy(out).to(device=x.device, dtype=x.dtype) if torch.is_tensor(x) else out
 
     @staticmethod
     def forwardTorchMulti(matrices: Sequence["RuntimeMatrix"], x: torch.Tensor,
                           biases: Sequence[torch.Tensor | None] | None = None) -> list[torch.Tensor]:
         """``[m.forward(x) (+ bias) for m in matrices]`` for matrices that read
-        the same fp16 CUDA activations, in one decode launch per run of equal
-        widths (up to four matrices; up to 16 activation rows, or 64 where the
-        decode kernel is the faster route).  No
-        single-call counterpart in the reference (its Stage-2F concatenates
-        the materialized weights, stage2f.py:382-420)."""
-        native = _requireNative()
-        return native.forward_torch_multi([m._native for m in matrices], x, biases)
+        the same fp16 activations, in one decode launch per run of equal
+        widths (up to four matrices).  No single-call counterpart in the
+        reference (its Stage-2F concatenates materialized weights,
+        stage2f.py:382-420)."""
+        return _requireNative().forward_torch_multi([m._native for m in matrices], x, biases)
 
     def benchmark(self, x: Any, iterations: int = 500) -> float:
-        if torch.is_tensor(x):
-            x = x.detach().float().cpu().numpy()
-        values = np.ascontiguousarray(np.asarray(x, dtype=np.float32).reshape(-1))
-        return float(self._native.benchmark(values, int(iterations)))
+        host = x.detach().to("cpu", torch.float32).numpy() if torch.is_tensor(x) else x
+        row = np.ascontiguousarray(np.asarray(host, dtype=np.float32).reshape(-1))
+        return float(self._native.benchmark(row, int(iterations)))
 
     def dequantize(self) -> np.ndarray:
         return np.asarray(self._native.dequantize(), dtype=np.float32)
 
     def _materializeTorch(self) -> torch.Tensor:
         return self._native._materializeTorch()
+
+    def _residentFp16(self) -> torch.Tensor:
+        """The decoded fp16 weights, materialized once and kept: what the
+        reference's execution holds for b = 9..16 (runtime.cu:989-999)."""
+        if self._resident is None:
+            self._resident = self._materializeTorch()
+        return self._resident
+
+    def _releaseResident(self) -> None:
+        self._resident = None
 
     def save(self, path: str | Path) -> None:
         self._native.save(str(path))
@@ -323,75 +358,32 @@ class RuntimeMatrix:
         return self
 
     @property
-    def rows(self) -> int:
-        return int(self._native.rows)
-
-    @property
-    def cols(self) -> int:
-        return int(self._native.cols)
-
-    @property
     def shape(self) -> tuple[int, int]:
         return tuple(int(v) for v in self._native.shape)
 
-    @property
-    def storageBits(self) -> int:
-        return int(self._native.storageBits)
 
-    @property
-    def executionWidth(self) -> int:
-        return int(self._native.executionWidth)
+for _name, _cast in (("rows", int), ("cols", int), ("storageBits", int), ("executionWidth", int),
+                     ("storageBytes", int), ("executionBytes", int), ("originalBytes", int),
+                     ("executionPlanner", str), ("decodePolicy", str), ("activateDType", str),
+                     ("memoryReduction", float), ("threshold", float), ("error", float)):
+    setattr(RuntimeMatrix, _name, _native_reader(_name, _cast))
+del _name, _cast
 
-    @property
-    def executionPlanner(self) -> str:
-        return str(self._native.executionPlanner)
 
-    @property
-    def decodePolicy(self) -> str:
-        return str(self._native.decodePolicy)
-
-    @property
-    def activateDType(self) -> str:
-        return str(self._native.activateDType)
-
-    @property
-    def storageBytes(self) -> int:
-        return int(self._native.storageBytes)
-
-    @property
-    def executionBytes(self) -> int:
-        return int(self._native.executionBytes)
-
-    @property
-    def originalBytes(self) -> int:
-        return int(self._native.originalBytes)
-
-    @property
-    def memoryReduction(self) -> float:
-        return float(self._native.memoryReduction)
-
-    @property
-    def threshold(self) -> float:
-        return float(self._native.threshold)
-
-    @property
-    def error(self) -> float:
-        return float(self._native.error)
-
+# -- the compressed Linear ---------------------------------------------------------
 
 class _RouteOwner:
-    """Holds the planner's frozen route for one phase of one layer."""
+    """Carries the planner's frozen route for one phase of one layer."""
 
     __slots__ = ("_mlbricks_frozen_auto_routes", "_mlbricks_frozen_auto_details", "_mlbricks_auto_route_cache")
 
     def __init__(self) -> None:
-        self._mlbricks_frozen_auto_routes: dict = {}
-        self._mlbricks_frozen_auto_details: dict = {}
-        self._mlbricks_auto_route_cache = None
+        EXECUTION_PLANNER.clear_owner_routes(self)
 
 
 class _ElasticLinear(nn.Module):
-    """Compressed Linear (core.py:427-471), routed through the execution planner."""
+    """A Linear whose weight is an ElasticBit matrix (core.py:427-471); every
+    call goes through the planner (``backend``: auto / native / pytorch)."""
 
     def __init__(self, matrix: RuntimeMatrix, inFeatures: int, outFeatures: int,
                  bias: torch.Tensor | None, backend: str = "auto") -> None:
@@ -413,54 +405,72 @@ class _ElasticLinear(nn.Module):
         return self
 
     def resolved_backend(self) -> str:
-        routes = {phase: EXECUTION_PLANNER.owner_routes(owner) for phase, owner in self._routeOwners.items()}
-        frozen = {phase: next(iter(r.values())) for phase, r in routes.items() if r}
         if self.backend != "auto":
             return self.backend
-        if not frozen:
-            return "auto"
-        return ",".join(f"{phase}={route}" for phase, route in sorted(frozen.items()))
+        frozen = []
+        for phase in sorted(self._routeOwners):
+            routes = EXECUTION_PLANNER.owner_routes(self._routeOwners[phase])
+            if routes:
+                frozen.append(f"{phase}={next(iter(routes.values()))}")
+        return ",".join(frozen) or "auto"
+
+    def _bias_as(self, x: torch.Tensor) -> torch.Tensor | None:
+        if self.bias is None:
+            return None
+        return self.bias.to(device=x.device, dtype=x.dtype)
 
     def _forwardNative(self, x: torch.Tensor) -> torch.Tensor:
-        bias = self.bias
-        if bias is not None and (bias.dtype != torch.float16 or bias.device != x.device):
-            bias = bias.to(device=x.device, dtype=torch.float16)
-        return self.matrix._native.forwardTorch(x, bias=bias)
+        return self.matrix._native.forwardTorch(x, bias=self._bias_as(x))
 
     def _forwardPytorch(self, x: torch.Tensor) -> torch.Tensor:
-        weight = self.matrix._materializeTorch()
+        """The reference's prefill route (core.py:462-471): F.linear on the
+        decoded fp16 weights, resident for b >= 9, materialized per call
+        below."""
+        weight = (self.matrix._residentFp16() if self.matrix.storageBits >= _RESIDENT_MIN_BITS
+                  else self.matrix._materializeTorch())
         if weight.device != x.device:
             raise RuntimeError("ElasticBit Linear expects activations on the device that holds its matrix")
-        if weight.dtype != x.dtype:
-            weight = weight.to(dtype=x.dtype)
-        bias = self.bias
-        if bias is not None and (bias.device != x.device or bias.dtype != x.dtype):
-            bias = bias.to(device=x.device, dtype=x.dtype)
-        return F.linear(x, weight, bias)
+        return F.linear(x, weight.to(dtype=x.dtype), self._bias_as(x))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if x.shape[-1] != self.inFeatures:
             raise ValueError(f"ElasticBit Linear expected last dimension {self.inFeatures}, got {x.shape[-1]}")
+        hip_ok = (_nativeAvailable() and x.is_cuda and x.dtype == torch.float16
+                  and self.matrix._native.deviceIndex == x.get_device())
         rows = x.numel() // self.inFeatures
-        native_ok = (_nativeAvailable() and x.is_cuda and x.dtype == torch.float16
-                     and self.matrix._native.deviceIndex == x.get_device())
-        training = bool(torch.is_grad_enabled() and x.requires_grad)
-        phase = "decode" if rows <= _DECODE_MAX_ROWS else "prefill"
-        xc = x.contiguous() if native_ok else x
+        phase = "decode" if rows <= DECODE_PHASE_ROWS else "prefill"
+        owner = self._routeOwners[phase]
+        xc = x.contiguous() if hip_ok else x
         route = EXECUTION_PLANNER.qualify_operator_once(
-            self._routeOwners[phase], "elastic_linear", xc,
+            owner, "elastic_linear", xc,
             {"native": lambda: self._forwardNative(xc), "pytorch": lambda: self._forwardPytorch(x)},
-            requested_backend=self.backend, native_available=native_ok, training=training,
+            requested_backend=self.backend, native_available=hip_ok,
+            training=bool(torch.is_grad_enabled() and x.requires_grad),
             extra=(self.outFeatures, self.inFeatures, self.matrix.storageBits, phase),
             default_auto="pytorch",
         )
         if route == "native":
+            self._drop_unused_resident()
             return self._forwardNative(xc)
         return self._forwardPytorch(x)
 
+    def _drop_unused_resident(self) -> None:
+        """A resident fp16 copy made for the qualification race stays only
+        while some phase of this layer runs the PyTorch route."""
+        if self.matrix._resident is None:
+            return
+        for owner in self._routeOwners.values():
+            if "pytorch" in EXECUTION_PLANNER.owner_routes(owner).values():
+                return
+        if self.backend != "pytorch":
+            self.matrix._releaseResident()
+
+
+# -- model-level controller ----------------------------------------------------------
 
 class _ModelElasticBit:
-    """``model.elasticbit`` controller (core.py:474-547)."""
+    """``model.elasticbit`` (core.py:474-547): what was compressed, the decode
+    policy, and a summary table."""
 
     def __init__(self, model: nn.Module, threshold: float, decodePolicy: str, compressedNames: Sequence[str],
                  skippedNames: Sequence[str], optimizationProfiles: Mapping[str, Any] | None = None) -> None:
@@ -473,80 +483,234 @@ class _ModelElasticBit:
         self.activeOptimization: dict[str, Any] | None = None
 
     def _layers(self) -> list[tuple[str, _ElasticLinear]]:
-        modules = dict(self._model.named_modules())
-        return [(n, modules[n]) for n in self.compressedNames if isinstance(modules.get(n), _ElasticLinear)]
+        found = []
+        for name in self.compressedNames:
+            try:
+                layer = self._model.get_submodule(name)
+            except AttributeError:
+                continue
+            if isinstance(layer, _ElasticLinear):
+                found.append((name, layer))
+        return found
+
+    def _matrices(self) -> list[RuntimeMatrix]:
+        """Each distinct matrix once (shared weights share one)."""
+        unique: dict[int, RuntimeMatrix] = {}
+        for _, layer in self._layers():
+            unique.setdefault(id(layer.matrix), layer.matrix)
+        return list(unique.values())
 
     def setDecodePolicy(self, decodePolicy: str) -> "_ModelElasticBit":
         policy = _checkPolicy(decodePolicy)
-        seen: set[int] = set()
-        for _, layer in self._layers():
-            if id(layer.matrix) in seen:
-                continue
-            layer.matrix.setDecodePolicy(policy)
-            seen.add(id(layer.matrix))
+        for matrix in self._matrices():
+            matrix.setDecodePolicy(policy)
         self.decodePolicy = policy
         return self
 
     def summary(self) -> str:
-        backend = ElasticBit.backend()
-        lines = [
-            "ElasticBit Summary",
-            "-" * 60,
-            f"Threshold       : {self.threshold}",
-            f"Decode Policy   : {self.decodePolicy}",
-            f"Backend         : {backend.architecture or 'unavailable'}",
-            f"Prefill         : {backend.prefill or 'unknown'}",
-            f"Decode Engine   : {backend.decodeEngine or 'unknown'}",
-            f"Decode Status   : {backend.decodeStatus or 'unknown'}",
-            f"Decode Planner  : {backend.decodePlanner or 'unknown'}",
-            f"Decode Validate : {backend.decodeValidation or 'unknown'}",
-            f"Activate DType  : {backend.activateDType or 'unknown'}",
-            "",
-            f"{'Layer':36s} {'Stored':>8s} {'Execute':>10s} {'Planner':>14s} {'Error':>10s}",
+        info = ElasticBit.backend()
+        header = [
+            ("Threshold", self.threshold), ("Decode Policy", self.decodePolicy),
+            ("Backend", info.architecture or "unavailable"), ("Prefill", info.prefill or "unknown"),
+            ("Decode Engine", info.decodeEngine or "unknown"), ("Decode Status", info.decodeStatus or "unknown"),
+            ("Decode Planner", info.decodePlanner or "unknown"),
+            ("Decode Validate", info.decodeValidation or "unknown"),
+            ("Activate DType", info.activateDType or "unknown"),
         ]
+        lines = ["ElasticBit Summary", "-" * 60]
+        lines += [f"{label:<16s}: {value}" for label, value in header]
+        lines += ["", f"{'Layer':36s} {'Stored':>8s} {'Execute':>10s} {'Planner':>14s} {'Error':>10s}"]
         for name, layer in self._layers():
             m = layer.matrix
-            lines.append(f"{name[:36]:36s} {str(m.storageBits) + '-bit':>8s} "
-                         f"{'W' + str(m.executionWidth) + 'A16':>10s} {m.executionPlanner:>14s} {m.error:10.6f}")
+            lines.append(f"{name[:36]:36s} {f'{m.storageBits}-bit':>8s} {f'W{m.executionWidth}A16':>10s} "
+                         f"{m.executionPlanner:>14s} {m.error:10.6f}")
         if self.skippedNames:
-            lines.extend(["", "Uncompressed (no safe calibration path):"])
-            lines.extend(f"  {n}" for n in self.skippedNames)
+            lines += ["", "Uncompressed (no safe calibration path):"] + [f"  {n}" for n in self.skippedNames]
         text = "\n".join(lines)
         print(text)
         return text
 
 
 def _semanticOutputWeightIds(model: nn.Module) -> set[int]:
-    """Weights of the model's token-output head via ``get_output_embeddings()`` (core.py:550-568)."""
+    """The token-output head's weight, found through the model's own
+    ``get_output_embeddings()`` rather than by module names (core.py:550-568)."""
     getter = getattr(model, "get_output_embeddings", None)
-    if not callable(getter):
-        return set()
     try:
-        output = getter()
+        head = getter() if callable(getter) else None
     except Exception:
-        return set()
-    if isinstance(output, nn.Linear):
-        return {id(output.weight)}
-    return set()
+        head = None
+    return {id(head.weight)} if isinstance(head, nn.Linear) else set()
 
+
+# -- compression pipeline ---------------------------------------------------------------
+
+class _CalibrationTap:
+    """Forward pre-hooks that keep the first CALIBRATION_ROWS input rows each
+    hooked Linear sees, as float32 host arrays."""
+
+    def __init__(self, linears: Mapping[str, nn.Linear]) -> None:
+        self._linears = dict(linears)
+        self._rows: dict[str, list[np.ndarray]] = {name: [] for name in self._linears}
+        self._kept: dict[str, int] = {name: 0 for name in self._linears}
+        self._handles: list[Any] = []
+
+    def _hook(self, name: str):
+        def capture(_module: nn.Module, inputs: tuple[Any, ...]) -> None:
+            room = CALIBRATION_ROWS - self._kept[name]
+            if room <= 0 or not inputs or not torch.is_tensor(inputs[0]):
+                return
+            flat = inputs[0].detach().reshape(-1, inputs[0].shape[-1])[:room]
+            self._rows[name].append(flat.to("cpu", torch.float32).numpy().copy())
+            self._kept[name] += flat.shape[0]
+        return capture
+
+    def __enter__(self) -> "_CalibrationTap":
+        self._handles = [linear.register_forward_pre_hook(self._hook(name))
+                         for name, linear in self._linears.items()]
+        return self
+
+    def __exit__(self, *exc: Any) -> None:
+        for handle in self._handles:
+            handle.remove()
+        self._handles = []
+
+    def rows_for(self, names: Sequence[str]) -> np.ndarray | None:
+        """The captured rows of every use of one weight, in name order."""
+        parts = [block for name in names for block in self._rows.get(name, [])]
+        return np.ascontiguousarray(np.concatenate(parts), dtype=np.float32) if parts else None
+
+    def forget(self, names: Iterable[str]) -> None:
+        for name in names:
+            self._rows.pop(name, None)
+
+
+@dataclass
+class _WeightGroup:
+    """Every Linear name that uses one weight tensor (in module order)."""
+    weight_id: int
+    names: list[str]
+
+
+def _weight_groups(model: nn.Module) -> list[_WeightGroup]:
+    groups: dict[int, _WeightGroup] = {}
+    for name, module in model.named_modules():
+        if isinstance(module, nn.Linear):
+            groups.setdefault(id(module.weight), _WeightGroup(id(module.weight), [])).names.append(name)
+    return list(groups.values())
+
+
+def _progress_enabled() -> bool:
+    return os.environ.get("MLBRICKS_ELASTICBIT_PROGRESS", "").strip().lower() in {"1", "true", "yes", "on"}
+
+
+def _free_vram(device: torch.device) -> str:
+    free, total = torch.cuda.mem_get_info(device)
+    return f"free={free / 2**30:.2f}/{total / 2**30:.2f} GiB"
+
+
+def _matrix_for(linear: nn.Linear, calibration: np.ndarray, threshold: float, policy: str,
+                report: Callable[[str], None]) -> RuntimeMatrix:
+    """Select the width of one Linear's weight and build its matrix on the
+    weight's device: packed from the analyzer's codes for b <= 15, the fp16
+    values themselves for the fallback."""
+    bits, err, codes, scales = _selectBitsTorch(linear.weight, calibration, threshold, codesOnDevice=True)
+    torch.cuda.empty_cache()      # hand the analysis blocks back before the runtime allocates
+    report(f"selected {bits}-bit error={err:.6g}")
+    with torch.cuda.device(linear.weight.device):
+        if bits <= 15:
+            return RuntimeMatrix._compressSelectedCodesTorch(codes, scales, bits, threshold, err, decodePolicy=policy)
+        fp16 = _matrix_f32(linear.weight, "weights")
+        return RuntimeMatrix._compressSelected(fp16, bits, threshold, err, decodePolicy=policy)
+
+
+def _install(model: nn.Module, names: Sequence[str], matrix: RuntimeMatrix, device: torch.device) -> None:
+    """Replace every Linear of one weight group by an _ElasticLinear sharing
+    ``matrix`` (so the group's fp16 weight can be freed at once)."""
+    for name in names:
+        current = model.get_submodule(name)
+        if not isinstance(current, nn.Linear):
+            raise RuntimeError(f"ElasticBit expected Linear module at {name}")
+        layer = _ElasticLinear(matrix, current.in_features, current.out_features, current.bias)
+        _replaceNamedModule(model, name, layer.to(device=device))
+
+
+# -- the zip artifact ---------------------------------------------------------------------
+
+class _Artifact:
+    """``manifest.json``, ``matrices/matrix_%05d.mlb`` (MLB4) and ``state.pt``
+    in one DEFLATE zip (core.py:900-1017)."""
+
+    MANIFEST = "manifest.json"
+    STATE = "state.pt"
+    MATRICES = "matrices"
+
+    @classmethod
+    def write(cls, model: nn.Module, controller: _ModelElasticBit, path: Path) -> None:
+        files: dict[int, str] = {}
+        layers = []
+        with zipfile.ZipFile(path, "w", compression=zipfile.ZIP_DEFLATED) as archive, \
+                tempfile.TemporaryDirectory(prefix="elasticbit-save-") as scratch:
+            for name in controller.compressedNames:
+                try:
+                    layer = model.get_submodule(name)
+                except AttributeError:
+                    layer = None
+                if not isinstance(layer, _ElasticLinear):
+                    raise RuntimeError(f"ElasticBit layer disappeared before save: {name}")
+                member = files.get(id(layer.matrix))
+                if member is None:
+                    member = files[id(layer.matrix)] = f"matrix_{len(files):05d}.mlb"
+                    staged = Path(scratch) / member
+                    layer.matrix.save(staged)
+                    archive.write(staged, f"{cls.MATRICES}/{member}")
+                layers.append({"name": name, "matrix": member, "inFeatures": layer.inFeatures,
+                               "outFeatures": layer.outFeatures, "hasBias": layer.bias is not None})
+            manifest = {"format": ARTIFACT_FORMAT[0], "version": ARTIFACT_FORMAT[1],
+                        "threshold": controller.threshold, "decodePolicy": controller.decodePolicy,
+                        "compressedNames": list(controller.compressedNames),
+                        "skippedNames": list(controller.skippedNames),
+                        "optimizationProfiles": controller.optimizationProfiles, "layers": layers}
+            archive.writestr(cls.MANIFEST, json.dumps(manifest, indent=2))
+            state = io.BytesIO()
+            torch.save(model.state_dict(), state)
+            archive.writestr(cls.STATE, state.getvalue())
+
+    @classmethod
+    def read_manifest(cls, archive: zipfile.ZipFile) -> dict[str, Any]:
+        manifest = json.loads(archive.read(cls.MANIFEST).decode("utf-8"))
+        if (manifest.get("format"), manifest.get("version")) != ARTIFACT_FORMAT:
+            raise ValueError("Unsupported ElasticBit model artifact")
+        return manifest
+
+    @classmethod
+    def load_matrix(cls, archive: zipfile.ZipFile, member: str, policy: str, device: torch.device) -> RuntimeMatrix:
+        with tempfile.TemporaryDirectory(prefix="elasticbit-load-") as scratch:
+            staged = Path(scratch) / "matrix.mlb"
+            staged.write_bytes(archive.read(f"{cls.MATRICES}/{member}"))
+            with torch.cuda.device(device):
+                return RuntimeMatrix.load(staged, decodePolicy=policy)
+
+    @classmethod
+    def load_state(cls, archive: zipfile.ZipFile, device: torch.device) -> dict[str, Any]:
+        return torch.load(io.BytesIO(archive.read(cls.STATE)), map_location=device, weights_only=True)
+
+
+# -- public namespace -------------------------------------------------------------------------
 
 class ElasticBit:
-    """Public namespace (core.py:571-1017)."""
+    """The public ElasticBit namespace (core.py:571-1017)."""
 
     RuntimeMatrix = RuntimeMatrix
 
     @staticmethod
     def analyze(weights: Any, calibrationData: Any, threshold: float) -> BitAnalysis:
-        native = _requireNative()
-        w = _toNumpy2D(weights, name="weights")
-        c = _toNumpy2D(calibrationData, name="calibrationData")
-        raw = native.analyze(w, c, float(threshold))
-        candidates = tuple(
-            BitCandidate(bits=int(i["bits"]), hardwareNativeError=float(i["hardwareNativeError"]),
-                         fullPrecisionError=float(i["fullPrecisionError"]), error=float(i["error"]),
-                         storageBytes=int(i["storageBytes"]), memoryReduction=float(i["memoryReduction"]),
-                         passes=bool(i["passes"]))
-            for i in raw["candidates"])
+        """The host analyzer's errors for every width (runtime.cu:280-483)."""
+        raw = _requireNative().analyze(_matrix_f32(weights, "weights"),
+                                       _matrix_f32(calibrationData, "calibrationData"), float(threshold))
+        types = {f.name: f.type for f in fields(BitCandidate)}
+        casts = {"int": int, "float": float, "bool": bool}
+        candidates = tuple(BitCandidate(**{key: casts[types[key]](item[key]) for key in types})
+                           for item in raw["candidates"])
         return BitAnalysis(threshold=float(raw["threshold"]), selectedBits=int(raw["selectedBits"]),
                            selectedError=float(raw["selectedError"]), candidates=candidates)
 
@@ -563,24 +727,16 @@ class ElasticBit:
     def backend() -> BackendInfo:
         if not _nativeAvailable():
             err = _nativeImportError()
-            return BackendInfo(available=False, device=None, deviceIndex=None, architecture=None,
-                               weightWidths=(), activateDType=None, prefill=None, decodePlanner=None,
-                               decodeEngine=None, decodeStatus=None, decodeValidation=None, validated=False,
-                               error=None if err is None else str(err))
+            return _unavailable_backend(None if err is None else str(err))
         raw = _requireNative().backendInfo()
         if not raw["available"]:
-            return BackendInfo(available=False, device=None, deviceIndex=None, architecture=None,
-                               weightWidths=tuple(raw["weightWidths"]), activateDType=raw["activateDType"],
-                               prefill=None, decodePlanner=None, decodeEngine=None, decodeStatus=None,
-                               decodeValidation=None, validated=False,
-                               error="no HIP device is visible to the ElasticBit runtime")
-        return BackendInfo(available=True, device=str(raw["device"]), deviceIndex=int(raw["deviceIndex"]),
-                           architecture=str(raw["architecture"]),
+            return _unavailable_backend("no HIP device is visible to the ElasticBit runtime",
+                                        raw["weightWidths"], raw["activateDType"])
+        text = ("device", "architecture", "activateDType", "prefill", "decodePlanner", "decodeEngine",
+                "decodeStatus", "decodeValidation")
+        return BackendInfo(available=True, deviceIndex=int(raw["deviceIndex"]),
                            weightWidths=tuple(int(v) for v in raw["weightWidths"]),
-                           activateDType=str(raw["activateDType"]), prefill=str(raw["prefill"]),
-                           decodePlanner=str(raw["decodePlanner"]), decodeEngine=str(raw["decodeEngine"]),
-                           decodeStatus=str(raw["decodeStatus"]), decodeValidation=str(raw["decodeValidation"]),
-                           validated=bool(raw["validated"]))
+                           validated=bool(raw["validated"]), **{key: str(raw[key]) for key in text})
 
     @staticmethod
     def optimize(model: nn.Module, force: bool = False) -> nn.Module:
@@ -596,99 +752,65 @@ class ElasticBit:
     @staticmethod
     def compress(model: nn.Module, calibrationData: Any, threshold: float, decodePolicy: str = "hardwareNative",
                  preserveOutputHead: bool = True) -> nn.Module:
-        """Compress every unprotected fp16 nn.Linear of ``model`` (core.py:695-898)."""
+        """Compress every fp16 ``nn.Linear`` of ``model`` except embeddings and
+        the output head (core.py:695-898).
+
+        The calibration batches run once through the model; each Linear keeps
+        its first 32 input rows.  A weight shared by several Linears is
+        analysed once on all their rows and becomes one shared matrix.  Each
+        weight group is replaced as soon as its matrix exists, so peak device
+        memory stays near the compressed model's."""
         if not isinstance(model, nn.Module):
             raise TypeError("ElasticBit.compress() expects a torch.nn.Module")
         _requireNative()
         policy = _checkPolicy(decodePolicy)
-        batches = _toCalibrationBatches(calibrationData)
-        device = _moduleDevice(model)
+        batches = _batch_list(calibrationData)
+        device = _device_of(model)
         if device.type != "cuda":
             raise RuntimeError("ElasticBit model compression currently requires a CUDA model")
-        for module in model.modules():
-            if isinstance(module, nn.Linear) and module.weight.dtype != torch.float16:
-                raise RuntimeError("ElasticBit.compress() currently requires FP16 Linear weights. "
-                                   "Convert the model to float16 before compression.")
+        linears = {name: m for name, m in model.named_modules() if isinstance(m, nn.Linear)}
+        if any(m.weight.dtype != torch.float16 for m in linears.values()):
+            raise RuntimeError("ElasticBit.compress() currently requires FP16 Linear weights. "
+                               "Convert the model to float16 before compression.")
+        head_ids = _semanticOutputWeightIds(model) if preserveOutputHead else set()
+        protected = head_ids | {id(m.weight) for m in model.modules() if isinstance(m, nn.Embedding)}
 
-        embedding_ids = {id(m.weight) for m in model.modules() if isinstance(m, nn.Embedding)}
-        output_ids = _semanticOutputWeightIds(model) if bool(preserveOutputHead) else set()
-        protected = embedding_ids | output_ids
-
-        collected: dict[str, list[np.ndarray]] = {}
-        max_rows = 32          # calibration rows kept per Linear (core.py:734)
-
-        def make_hook(name: str):
-            def hook(_module: nn.Module, inputs: tuple[Any, ...]) -> None:
-                if not inputs or not torch.is_tensor(inputs[0]):
-                    return
-                rows = inputs[0].detach().float().reshape(-1, inputs[0].shape[-1])
-                remaining = max_rows - sum(a.shape[0] for a in collected.get(name, []))
-                if remaining <= 0:
-                    return
-                collected.setdefault(name, []).append(rows[:remaining].cpu().numpy().astype(np.float32, copy=True))
-            return hook
-
-        handles = []
-        linears: list[tuple[str, nn.Linear]] = []
-        for name, module in model.named_modules():
-            if isinstance(module, nn.Linear):
-                linears.append((name, module))
-                if id(module.weight) not in protected:
-                    handles.append(module.register_forward_pre_hook(make_hook(name)))
-        model.eval()
-        try:
-            with torch.inference_mode():
-                for batch in batches:
-                    _callModel(model, _moveBatch(batch, device))
-        finally:
-            for h in handles:
-                h.remove()
-
-        names_by_weight: dict[int, list[str]] = {}
-        for name, module in linears:
-            names_by_weight.setdefault(id(module.weight), []).append(name)
+        tap = _CalibrationTap({name: m for name, m in linears.items() if id(m.weight) not in protected})
         del linears
-        compressed: list[str] = []
-        skipped: list[str] = [n for wid, names in names_by_weight.items() if wid in output_ids for n in names]
-        progress = os.environ.get("MLBRICKS_ELASTICBIT_PROGRESS", "").strip().lower() in {"1", "true", "yes", "on"}
-        work = [(wid, names) for wid, names in names_by_weight.items() if wid not in protected]
+        model.eval()
+        with tap, torch.inference_mode():
+            for batch in batches:
+                _feed(model, _on_device(batch, device))
 
-        for index, (_, names) in enumerate(work, start=1):
-            module = model.get_submodule(names[0])
-            if not isinstance(module, nn.Linear):
-                raise RuntimeError(f"ElasticBit expected Linear module at {names[0]}")
-            samples = [a for n in names for a in collected.get(n, [])]
-            if not samples:
-                skipped.extend(names)
+        groups = _weight_groups(model)
+        skipped = [name for g in groups if g.weight_id in head_ids for name in g.names]
+        work = [g for g in groups if g.weight_id not in protected]
+        compressed: list[str] = []
+        chatty = _progress_enabled()
+        for index, group in enumerate(work, start=1):
+            def report(message: str, index: int = index) -> None:
+                if chatty:
+                    print(f"[ElasticBit] {index}/{len(work)} {message}", flush=True)
+
+            linear = model.get_submodule(group.names[0])
+            if not isinstance(linear, nn.Linear):
+                raise RuntimeError(f"ElasticBit expected Linear module at {group.names[0]}")
+            calibration = tap.rows_for(group.names)
+            if calibration is None:
+                skipped.extend(group.names)
                 continue
-            calibration = np.ascontiguousarray(np.concatenate(samples, axis=0), dtype=np.float32)
-            if progress:
-                print(f"[ElasticBit] {index}/{len(work)} analyzing {names[0]} "
-                      f"shape={tuple(module.weight.shape)} rows={calibration.shape[0]}", flush=True)
-            bits, err, codes, scales = _selectBitsTorch(module.weight, calibration, float(threshold),
-                                                        codesOnDevice=True)
-            if progress:
-                print(f"[ElasticBit] {index}/{len(work)} selected {bits}-bit error={err:.6g}", flush=True)
-            with torch.cuda.device(device):
-                if bits <= 15:
-                    matrix = RuntimeMatrix._compressSelectedCodesTorch(codes, scales, bits, float(threshold), err,
-                                                                       decodePolicy=policy)
-                else:
-                    weights = np.ascontiguousarray(module.weight.detach().cpu().float().numpy(), dtype=np.float32)
-                    matrix = RuntimeMatrix._compressSelected(weights, bits, float(threshold), err,
-                                                             decodePolicy=policy)
-            for name in names:
-                current = model.get_submodule(name)
-                if not isinstance(current, nn.Linear):
-                    raise RuntimeError(f"ElasticBit expected Linear module at {name}")
-                replacement = _ElasticLinear(matrix=matrix, inFeatures=current.in_features,
-                                             outFeatures=current.out_features, bias=current.bias).to(device=device)
-                _replaceNamedModule(model, name, replacement)
-                compressed.append(name)
-                collected.pop(name, None)
-            del module, codes, scales, calibration, samples, matrix
+            report(f"analyzing {group.names[0]} shape={tuple(linear.weight.shape)} rows={calibration.shape[0]} "
+                   f"{_free_vram(device)}" if chatty else "")
+            matrix = _matrix_for(linear, calibration, float(threshold), policy, report)
+            del linear, calibration
+            _install(model, group.names, matrix, device)
+            compressed.extend(group.names)
+            tap.forget(group.names)
+            del matrix
             gc.collect()
             torch.cuda.empty_cache()
+            if chatty:
+                report(f"packed/replaced {_free_vram(device)}")
 
         model.elasticbit = _ModelElasticBit(model, threshold=float(threshold), decodePolicy=policy,
                                             compressedNames=compressed, skippedNames=skipped)
@@ -696,94 +818,54 @@ class ElasticBit:
 
     @staticmethod
     def save(model: nn.Module, path: str | Path) -> Path:
-        """Zip artifact: manifest.json, matrices/matrix_%05d.mlb, state.pt (core.py:900-955)."""
+        """Write the compressed model as one zip artifact (core.py:900-955)."""
         controller = getattr(model, "elasticbit", None)
         if not isinstance(controller, _ModelElasticBit):
             raise ValueError("ElasticBit.save() expects a model produced by ElasticBit.compress()")
         destination = Path(path)
         destination.parent.mkdir(parents=True, exist_ok=True)
-        modules = dict(model.named_modules())
-        with tempfile.TemporaryDirectory(prefix="elasticbit-save-") as tmp:
-            root = Path(tmp)
-            (root / "matrices").mkdir()
-            layers = []
-            saved: dict[int, str] = {}
-            for name in controller.compressedNames:
-                layer = modules.get(name)
-                if not isinstance(layer, _ElasticLinear):
-                    raise RuntimeError(f"ElasticBit layer disappeared before save: {name}")
-                file = saved.get(id(layer.matrix))
-                if file is None:
-                    file = f"matrix_{len(saved):05d}.mlb"
-                    layer.matrix.save(root / "matrices" / file)
-                    saved[id(layer.matrix)] = file
-                layers.append({"name": name, "matrix": file, "inFeatures": layer.inFeatures,
-                               "outFeatures": layer.outFeatures, "hasBias": layer.bias is not None})
-            manifest = {
-                "format": _MODEL_FORMAT,
-                "version": _MODEL_FORMAT_VERSION,
-                "threshold": controller.threshold,
-                "decodePolicy": controller.decodePolicy,
-                "compressedNames": list(controller.compressedNames),
-                "skippedNames": list(controller.skippedNames),
-                "optimizationProfiles": controller.optimizationProfiles,
-                "layers": layers,
-            }
-            (root / "manifest.json").write_text(json.dumps(manifest, indent=2), encoding="utf-8")
-            torch.save(model.state_dict(), root / "state.pt")
-            with zipfile.ZipFile(destination, "w", compression=zipfile.ZIP_DEFLATED) as archive:
-                for file in sorted(root.rglob("*")):
-                    if file.is_file():
-                        archive.write(file, file.relative_to(root).as_posix())
+        _Artifact.write(model, controller, destination)
         return destination
 
     @staticmethod
     def load(model: nn.Module, path: str | Path, decodePolicy: str = "hardwareNative") -> nn.Module:
-        """Rebuild compressed layers into an architecture instance (core.py:957-1017)."""
+        """Rebuild the compressed layers of an artifact into an instance of the
+        original architecture, then load its state (core.py:957-1017)."""
         if not isinstance(model, nn.Module):
             raise TypeError("ElasticBit.load() requires the model architecture as its first argument")
         _requireNative()
         source = Path(path)
         if not source.exists():
             raise FileNotFoundError(source)
-        with tempfile.TemporaryDirectory(prefix="elasticbit-load-") as tmp:
-            root = Path(tmp)
-            with zipfile.ZipFile(source, "r") as archive:
-                archive.extractall(root)
-            manifest = json.loads((root / "manifest.json").read_text(encoding="utf-8"))
-            if manifest.get("format") != _MODEL_FORMAT or manifest.get("version") != _MODEL_FORMAT_VERSION:
-                raise ValueError("Unsupported ElasticBit model artifact")
+        with zipfile.ZipFile(source, "r") as archive:
+            manifest = _Artifact.read_manifest(archive)
             policy = _checkPolicy(decodePolicy)
-            modules = dict(model.named_modules())
-            cache: dict[str, RuntimeMatrix] = {}
+            matrices: dict[str, RuntimeMatrix] = {}
             compressed: list[str] = []
             for entry in manifest["layers"]:
                 name = str(entry["name"])
-                target = modules.get(name)
+                try:
+                    target = model.get_submodule(name)
+                except AttributeError:
+                    target = None
                 if not isinstance(target, nn.Linear):
                     raise ValueError(f"Model architecture does not contain expected Linear layer: {name}")
                 device = target.weight.device
                 if device.type != "cuda":
                     raise RuntimeError("ElasticBit.load() requires the target model on CUDA")
-                file = str(entry["matrix"])
-                matrix = cache.get(file)
-                if matrix is None:
-                    with torch.cuda.device(device):
-                        matrix = RuntimeMatrix.load(root / "matrices" / file, decodePolicy=policy)
-                    cache[file] = matrix
-                replacement = _ElasticLinear(matrix=matrix, inFeatures=int(entry["inFeatures"]),
-                                             outFeatures=int(entry["outFeatures"]),
-                                             bias=target.bias if bool(entry["hasBias"]) else None).to(device=device)
-                _replaceNamedModule(model, name, replacement)
+                member = str(entry["matrix"])
+                if member not in matrices:
+                    matrices[member] = _Artifact.load_matrix(archive, member, policy, device)
+                layer = _ElasticLinear(matrices[member], int(entry["inFeatures"]), int(entry["outFeatures"]),
+                                       target.bias if bool(entry["hasBias"]) else None)
+                _replaceNamedModule(model, name, layer.to(device=device))
                 compressed.append(name)
-                modules[name] = replacement
-            state = torch.load(root / "state.pt", map_location=_moduleDevice(model), weights_only=True)
-            model.load_state_dict(state, strict=True)
-            model.elasticbit = _ModelElasticBit(model, threshold=float(manifest["threshold"]), decodePolicy=policy,
-                                                compressedNames=compressed,
-                                                skippedNames=tuple(manifest.get("skippedNames", ())),
-                                                optimizationProfiles=manifest.get("optimizationProfiles", {}))
-            return model
+            model.load_state_dict(_Artifact.load_state(archive, _device_of(model)), strict=True)
+        model.elasticbit = _ModelElasticBit(model, threshold=float(manifest["threshold"]), decodePolicy=policy,
+                                            compressedNames=compressed,
+                                            skippedNames=tuple(manifest.get("skippedNames", ())),
+                                            optimizationProfiles=manifest.get("optimizationProfiles", {}))
+        return model
 
 
 __all__ = ["ElasticBit", "RuntimeMatrix", "BitAnalysis", "BitCandidate", "BackendInfo"]

@@ -1,98 +1,109 @@
-"""Execution-backend policy: ``auto`` / ``native`` / ``pytorch``.
+"""Execution-backend policy shared by every backend-aware element.
 
-Same contract as ``mlbricks/runtime.py:28-94``: ``auto`` lets the planner
-qualify each backend-aware element once and freeze the winner, ``native``
-requires the HIP route (RuntimeError when it cannot run), ``pytorch`` always
-takes the PyTorch route.  Historical names are accepted as aliases.
+Three names (the contract of ``mlbricks/runtime.py``):
+
+* ``auto`` -- the planner qualifies each element on its first eligible call
+  and freezes the winner on that element;
+* ``native`` -- the HIP implementation is required (``RuntimeError`` when it
+  cannot serve a call);
+* ``pytorch`` -- the PyTorch implementation always.
+
+Older spellings are accepted and mapped onto these, with a
+``DeprecationWarning`` when the caller asks for one.
 """
 from __future__ import annotations
 
 import warnings
-from typing import Any
+from typing import Any, Iterator
 
 VALID_BACKENDS = frozenset({"auto", "native", "pytorch"})
 
-_LEGACY = {
-    "cuda": "native",
-    "hip": "native",
-    "cpp": "native",
-    "cpp/cuda": "native",
-    "torch": "pytorch",
-    "python": "pytorch",
-    "reference": "pytorch",
+# Historical names, grouped by the backend they stand for.
+_ALIASES_BY_BACKEND = {
+    "native": ("cuda", "hip", "rocm", "cpp", "cpp/cuda"),
+    "pytorch": ("torch", "python", "reference"),
 }
+_ALIAS = {alias: backend for backend, aliases in _ALIASES_BY_BACKEND.items() for alias in aliases}
 
 
 def normalize_backend(value: str | None = "auto", *, warn_legacy: bool = False) -> str:
-    """Return the canonical backend name (runtime.py:45-64)."""
+    """The canonical backend for ``value`` (None means ``auto``); case,
+    surrounding blanks and ``-`` versus ``_`` do not matter."""
     if value is None:
         return "auto"
-    name = str(value).strip().lower().replace("-", "_")
-    if name in VALID_BACKENDS:
-        return name
-    if name in _LEGACY:
-        mapped = _LEGACY[name]
-        if warn_legacy:
-            warnings.warn(
-                f"backend={value!r} is a legacy backend name; use backend={mapped!r} instead.",
-                DeprecationWarning,
-                stacklevel=3,
-            )
-        return mapped
-    raise ValueError(f"backend must be one of: auto, native, pytorch; got {value!r}.")
+    key = str(value).strip().lower().replace("-", "_")
+    if key in VALID_BACKENDS:
+        return key
+    backend = _ALIAS.get(key)
+    if backend is None:
+        raise ValueError(f"backend must be one of: auto, native, pytorch; got {value!r}.")
+    if warn_legacy:
+        warnings.warn(f"backend={value!r} is a legacy backend name; use backend={backend!r} instead.",
+                      DeprecationWarning, stacklevel=3)
+    return backend
+
+
+def _elements(module: Any, recursive: bool) -> Iterator[Any]:
+    """The module itself, then (when recursive) every descendant once."""
+    yield module
+    walk = getattr(module, "modules", None)
+    if recursive and callable(walk):
+        for child in walk():
+            if child is not module:
+                yield child
+
+
+def _assign(element: Any, backend: str) -> None:
+    """Give one element the backend: through its ``set_backend`` when it has
+    one (non-recursively, the walk covers its children), else its
+    ``backend`` attribute when it has one."""
+    setter = getattr(element, "set_backend", None)
+    if callable(setter):
+        try:
+            setter(backend, recursive=False)
+        except TypeError:
+            setter(backend)
+    elif hasattr(element, "backend"):
+        element.backend = backend
 
 
 def set_module_backend(module: Any, backend: str, *, recursive: bool = True) -> Any:
-    """Set ``backend`` on a module and its backend-aware children (runtime.py:67-94)."""
+    """Set ``backend`` on a module and, by default, on all its backend-aware
+    descendants (runtime.py:67-94).  Returns the module."""
     value = normalize_backend(backend)
-    setter = getattr(module, "set_backend", None)
-    if callable(setter):
-        try:
-            return setter(value, recursive=recursive)
-        except TypeError:
-            setter(value)
-    elif hasattr(module, "backend"):
-        module.backend = value
-    if recursive and hasattr(module, "modules"):
-        for child in module.modules():
-            if child is module:
-                continue
-            child_setter = getattr(child, "set_backend", None)
-            if callable(child_setter):
-                child_setter(value)
-            elif hasattr(child, "backend"):
-                child.backend = value
+    for element in _elements(module, recursive):
+        _assign(element, value)
     return module
 
 
+def _resolved(element: Any) -> str:
+    resolver = getattr(element, "resolved_backend", None)
+    if not callable(resolver):
+        return "dynamic"
+    try:
+        return str(resolver())
+    except TypeError:
+        return "dynamic-by-input"
+    except Exception:
+        return "unavailable"
+
+
 def backend_report(module: Any) -> list[dict[str, str]]:
-    """Requested / resolved backend of every backend-aware child (runtime.py:97-125)."""
-    rows: list[dict[str, str]] = []
-    named = getattr(module, "named_modules", None)
-    if not callable(named):
-        return rows
-    for name, child in named():
-        if child is module and not name:
+    """One row per backend-aware descendant: its name, class, requested and
+    resolved backend (runtime.py:97-125)."""
+    walk = getattr(module, "named_modules", None)
+    if not callable(walk):
+        return []
+    report = []
+    for name, element in walk():
+        if element is module and not name:
             continue
-        requested = getattr(child, "backend", None)
-        resolver = getattr(child, "resolved_backend", None)
-        if requested is None and not callable(resolver):
+        requested = getattr(element, "backend", None)
+        if requested is None and not callable(getattr(element, "resolved_backend", None)):
             continue
-        resolved = "dynamic"
-        if callable(resolver):
-            try:
-                resolved = str(resolver())
-            except TypeError:
-                resolved = "dynamic-by-input"
-            except Exception:
-                resolved = "unavailable"
-        rows.append({
-            "name": name or child.__class__.__name__,
-            "component": child.__class__.__name__,
-            "requested": str(requested or "auto"),
-            "resolved": resolved,
-        })
-    return rows
+        report.append({"name": name or type(element).__name__, "component": type(element).__name__,
+                       "requested": str(requested or "auto"), "resolved": _resolved(element)})
+    return report
 
 
 __all__ = ["VALID_BACKENDS", "normalize_backend", "set_module_backend", "backend_report"]

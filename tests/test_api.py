@@ -237,3 +237,110 @@ def test_training_calls_stay_on_pytorch():
 
     assert planner.qualify_operator_once(Owner(), "elastic_linear", x, {"native": lambda: x},
                                          native_available=True, training=True) == "pytorch"
+
+
+def test_operator_decisions_report_the_heuristic_and_benchmarks_override_it():
+    """As the reference's tests/test_unified_execution_planner.py: a first
+    auto call records the operator default with a 'heuristic:' reason; a
+    recorded benchmark replaces it and bumps the revision."""
+    planner = MLBricksExecutionPlanner()
+    x = torch.randn(1, 32, 16)
+    assert planner.select_operator("elastic_linear", x, native_available=True, training=False) == "pytorch"
+    rows = planner.operator_decisions()
+    assert len(rows) == 1 and rows[0]["route"] == "pytorch"
+    assert str(rows[0]["reason"]).startswith("heuristic:")
+    assert rows[0]["key"][:2] == ("op", "elastic_linear")
+    revision = planner.operator_revision
+    assert planner.record_operator_benchmark("elastic_linear", x, {"native": 0.2, "pytorch": 0.8},
+                                             training=False) == "native"
+    assert planner.operator_revision == revision + 1
+    assert planner.select_operator("elastic_linear", x, native_available=True, training=False) == "native"
+    assert len(planner.operator_cache) == 1
+    assert planner.operator_benchmarks[rows[0]["key"]] == {"native": 0.2, "pytorch": 0.8}
+    with pytest.raises(ValueError):
+        planner.record_operator_benchmark("elastic_linear", x, {"native": 0.0}, training=False)
+
+
+def test_select_operator_cached_is_sticky_until_a_decision_changes(monkeypatch):
+    planner = MLBricksExecutionPlanner()
+    x = torch.randn(2, 32, 16)
+    calls = {"n": 0}
+    original = planner.select_operator
+
+    def counted(*args, **kwargs):
+        calls["n"] += 1
+        return original(*args, **kwargs)
+
+    monkeypatch.setattr(planner, "select_operator", counted)
+
+    class Owner:
+        pass
+
+    owner = Owner()
+    ask = dict(requested_backend="auto", native_available=True, training=False, extra=(16,), default_auto="native")
+    assert planner.select_operator_cached(owner, "elastic_linear", x, **ask) == "native"
+    assert planner.select_operator_cached(owner, "elastic_linear", x, **ask) == "native"
+    assert calls["n"] == 1
+    planner.record_operator_benchmark("elastic_linear", x, {"native": 0.8, "pytorch": 0.2}, training=False,
+                                      extra=(16,))
+    assert planner.select_operator_cached(owner, "elastic_linear", x, **ask) == "pytorch"
+    assert calls["n"] == 2
+
+
+def test_parity_gate_compares_nested_outputs_leaf_by_leaf(monkeypatch):
+    planner = MLBricksExecutionPlanner()
+    x = torch.randn(2, 4, 8)
+    clock = _fake_clock(monkeypatch)
+
+    class Owner:
+        pass
+
+    def native():
+        clock["now"] += 0.001
+        return (x + 1.0e-6, {"state": x * 0.5 + 1.0e-6})
+
+    def pytorch():
+        clock["now"] += 0.002
+        return (x, {"state": x * 0.5})
+
+    owner = Owner()
+    assert planner.qualify_operator_once(owner, "nested", x, {"native": native, "pytorch": pytorch},
+                                         native_available=True, training=False, warmup=0, trials=3,
+                                         switch_margin=0.0) == "native"
+    details = owner._mlbricks_frozen_auto_details[("nested", False)]
+    assert details["parity"]["checked"] is True and details["parity"]["allclose"] is True
+    assert details["parity"]["tensor_leaves"] == 2
+    assert set(details["timings_ms"]) == {"native", "pytorch"}
+    assert details["reason"].startswith("correctness-pass;benchmark-once:")
+    # a different structure is a mismatch, whatever the speed
+    other = Owner()
+    assert planner.qualify_operator_once(other, "nested", x,
+                                         {"native": lambda: [x, {"state": x}], "pytorch": lambda: (x, {"state": x})},
+                                         native_available=True, training=False, default_auto="native") == "pytorch"
+    assert other._mlbricks_frozen_auto_details[("nested", False)]["parity"]["allclose"] is False
+
+
+def test_parity_gate_never_selects_native_when_the_reference_fails(monkeypatch):
+    planner = MLBricksExecutionPlanner()
+    x = torch.randn(2, 4, 8)
+    _fake_clock(monkeypatch)
+
+    class Owner:
+        pass
+
+    def broken():
+        raise RuntimeError("reference failed")
+
+    owner = Owner()
+    assert planner.qualify_operator_once(owner, "elastic_linear", x, {"native": lambda: x, "pytorch": broken},
+                                         native_available=True, training=False, default_auto="native") == "pytorch"
+    details = owner._mlbricks_frozen_auto_details[("elastic_linear", False)]
+    assert details["parity"]["checked"] is False and details["parity"]["allclose"] is None
+    assert "pytorch_reference" in details["errors"]
+    assert details["reason"] == "correctness-gate:reference-error;pytorch"
+
+
+def test_legacy_backend_names_warn_when_asked():
+    with pytest.warns(DeprecationWarning):
+        assert normalize_backend("cuda", warn_legacy=True) == "native"
+    assert normalize_backend(" Py-Torch ".replace("-", "")) == "pytorch"
