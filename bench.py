@@ -26,6 +26,11 @@ configs[4]'s compressed Linears, one decode token at a time:
 
     python bench.py --bolt-decode
 
+The read ceiling (a kernel that only reads) over a range of sizes, timed the
+same way (markdown table):
+
+    python bench.py --ceiling-curve
+
 Profiling helpers (same file, so the committed summaries name committed code):
 
     python bench.py --traffic-probe      # eager launches for rocprofv3 --pmc passes
@@ -56,6 +61,8 @@ COPY_CAL_KERNEL = "float16tofloat32_copy_kernel"
 DECODE_KERNEL = "linear_gemv_kernel"
 PREFILL_KERNEL = "linear_prefill"          # the 256 x 256 and the 128 x 256 tile kernels
 TRAFFIC_FILE = "decode_gemv_4096x4096_b10_m1_traffic.md"
+PROBE_SRC = ROOT / "probe_read.hip"
+PROBE_LIB = ROOT / "_build" / "libeb_probe_read.so"
 
 
 def log(msg: str) -> None:
@@ -83,6 +90,10 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--m-sweep", action="store_true",
                    help="time the forward over activation row counts 1..2048 on several shapes; "
                         "prints a markdown table")
+    p.add_argument("--ceiling-curve", action="store_true",
+                   help="time the pure-read probe over 21 MB .. 1 GiB with the headline's timing; "
+                        "prints a markdown table")
+    p.add_argument("--build-probe", action="store_true", help="compile probe_read.hip and exit")
     p.add_argument("--all-configs", action="store_true",
                    help="time every BASELINE configuration (0-3) beside the reference's execution format; "
                         "prints a markdown table")
@@ -132,9 +143,37 @@ def copies_of(layer, count: int):
             for _ in range(count)]
 
 
+_SPIN_CYCLES_PER_MS = None
+
+
+def _spin_cycles_per_ms() -> float:
+    """Clock cycles per millisecond of torch's spin kernel (torch.cuda._sleep),
+    measured once with HIP events."""
+    global _SPIN_CYCLES_PER_MS
+    if _SPIN_CYCLES_PER_MS is None:
+        import torch
+
+        probe = 2_000_000
+        torch.cuda._sleep(probe)
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        start.record()
+        torch.cuda._sleep(probe)
+        stop.record()
+        stop.synchronize()
+        _SPIN_CYCLES_PER_MS = probe / max(float(start.elapsed_time(stop)), 1e-3)
+    return _SPIN_CYCLES_PER_MS
+
+
 def time_graph(launches, steps: int, warmup: int) -> float:
     """Capture `steps` launches (cycling over `launches`) into one HIP graph, replay it
-    once untimed, then once between HIP events on the launch stream.  Returns ms."""
+    once untimed, then once between HIP events on the launch stream.  Returns ms.
+
+    Before the timed replay a spin kernel holds the stream for 1 ms plus 10 us
+    per step, so the host has queued the whole replay before the start event
+    executes: the events bracket exactly `steps` launches running back to
+    back, whatever `steps` is, and the host's enqueue cost stays outside."""
     import torch
 
     for i in range(warmup):
@@ -150,9 +189,11 @@ def time_graph(launches, steps: int, warmup: int) -> float:
     torch.cuda.synchronize()
     graph.replay()
     torch.cuda.synchronize()
+    hold = int(_spin_cycles_per_ms() * (1.0 + 0.01 * steps))
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
+        torch.cuda._sleep(hold)
         start.record(stream)
         graph.replay()
         stop.record(stream)
@@ -203,26 +244,53 @@ def bench_prefill(args) -> dict:
             "frac_fp16_mfma_peak": round(tflops / FP16_PEAK_TFLOPS, 4)}
 
 
+def build_probe(force: bool = False) -> Path:
+    """Compile probe_read.hip (bench.py's own read probe) for gfx950."""
+    import shutil
+    import subprocess
+
+    if PROBE_LIB.exists() and not force and PROBE_LIB.stat().st_mtime >= PROBE_SRC.stat().st_mtime:
+        return PROBE_LIB
+    PROBE_LIB.parent.mkdir(exist_ok=True)
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    tmp = PROBE_LIB.with_suffix(".so.tmp")
+    cmd = [hipcc, "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", str(PROBE_SRC), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"probe build failed: {res.stderr[-2000:]}")
+    os.replace(tmp, PROBE_LIB)
+    return PROBE_LIB
+
+
+# Launch shapes of the read probe's sweep: workgroups x threads, plain and
+# nontemporal loads (the probe rejects shapes needing > 512 B per thread).
+PROBE_SHAPES = tuple((b, t, nt) for nt in (0, 1)
+                     for b, t in ((256, 1024), (512, 1024), (512, 512), (1024, 256), (1024, 512), (1024, 1024),
+                                  (2048, 256), (2048, 512), (4096, 256)))
+
+
 def read_ceiling(nbytes: int, copies: int, steps: int, warmup: int) -> dict:
     """Best per-launch time of a kernel that only reads `nbytes` (the GEMV's
     algorithmic bytes), over `copies` rotated buffers, launched and timed
     exactly as the GEMV: the most any one-launch-per-step kernel over those
-    bytes reaches here.  Sweeps workgroup count and size."""
+    bytes reaches here.  Sweeps workgroup count and size, with plain and
+    nontemporal loads."""
     import ctypes
 
     import torch
 
-    lib = ctypes.CDLL(str(ROOT / "mlbricks_amd" / "lib" / "libeb_probe_read.so"))
-    lib.eb_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int, ctypes.c_int,
+    lib = ctypes.CDLL(str(build_probe()))
+    lib.eb_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                   ctypes.c_void_p, ctypes.c_void_p]
     size = -(-nbytes // 16) * 16
     bufs = [torch.empty(size, dtype=torch.uint8, device="cuda").random_(0, 255) for _ in range(copies)]
     sink = torch.zeros(1024, dtype=torch.int32, device="cuda")
     best = None
-    for blocks, threads in ((256, 1024), (512, 1024), (512, 512), (1024, 256), (1024, 512), (2048, 256)):
-        def mk(buf, blocks=blocks, threads=threads):
+    for blocks, threads, nt in PROBE_SHAPES:
+        def mk(buf, blocks=blocks, threads=threads, nt=nt):
             def launch():
-                rc = lib.eb_probe_read(buf.data_ptr(), size, blocks, threads, sink.data_ptr(),
+                rc = lib.eb_probe_read(buf.data_ptr(), size, blocks, threads, nt, sink.data_ptr(),
                                        torch.cuda.current_stream().cuda_stream)
                 if rc != 0:
                     raise RuntimeError(f"eb_probe_read: {rc}")
@@ -233,14 +301,32 @@ def read_ceiling(nbytes: int, copies: int, steps: int, warmup: int) -> dict:
             continue
         us = ms / steps * 1e3
         if best is None or us < best[0]:
-            best = (us, blocks, threads)
-    us, blocks, threads = best
+            best = (us, blocks, threads, nt)
+    us, blocks, threads, nt = best
     gbs = nbytes / (us * 1e-6) / 1e9
-    log(f"read ceiling: {us:.3f} us per {nbytes / 1e6:.1f} MB read ({gbs:.1f} GB/s, {blocks} x {threads})")
+    kind = "nontemporal" if nt else "plain"
+    log(f"read ceiling: {us:.3f} us per {nbytes / 1e6:.1f} MB read ({gbs:.1f} GB/s, {blocks} x {threads}, {kind})")
+    del bufs
     return {"us_per_launch": round(us, 3), "gbs": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
-            "launch": f"{blocks} workgroups x {threads} threads",
-            "what": "pure-read kernel (mlbricks_amd/csrc/probe_read.hip) over the GEMV's algorithmic bytes, "
+            "launch": f"{blocks} workgroups x {threads} threads, {kind} loads",
+            "what": "pure-read kernel (probe_read.hip) over the GEMV's algorithmic bytes, "
                     "same copy rotation and graph timing"}
+
+
+def ceiling_curve(args) -> int:
+    """The read probe's best time over a range of sizes, each rotated over at
+    least twice the MALL and timed like the headline: how much of a launch is
+    fixed cost and how close a read of a given size gets to the HBM peak."""
+    sizes = (4 << 20, 8 << 20, 21_004_288, 56_435_200, 128 << 20, 256 << 20, 1 << 30)
+    lines = ["| bytes per launch | us per launch | GB/s | % of 8 TB/s | best launch |", "|---|---|---|---|---|"]
+    for nbytes in sizes:
+        copies = max(2, -(-2 * MALL_BYTES // nbytes) + 1)
+        steps = max(20, min(args.steps, int(2e6 // max(nbytes >> 10, 1))))
+        r = read_ceiling(nbytes, copies, steps, max(3, steps // 10))
+        lines.append(f"| {nbytes:,} | {r['us_per_launch']:.3f} | {r['gbs']:.0f} | {100 * r['frac_hbm_peak']:.1f} | "
+                     f"{r['launch']} |")
+    print("\n".join(lines), flush=True)
+    return 0
 
 
 def reference_route(args) -> dict:
@@ -248,9 +334,11 @@ def reference_route(args) -> dict:
     methods (informational; never `value`).  Decode: at b = 9..15 the
     reference executes W16A16 (elasticbit_runtime.cu:240-244,1174-1178), a
     GEMV over fp16 weights, 2 bytes per weight; here that is this build's
-    GEMV kernel over b = 16 storage of the same weights.  Prefill: the
-    reference materializes fp16 weights and calls F.linear (core.py:462-471);
-    here materialize_kernel plus torch.matmul (hipBLASLt)."""
+    GEMV kernel over b = 16 storage of the same weights.  Prefill: at
+    b = 9..15 the reference keeps the fp16 weights resident and hands
+    F.linear a zero-copy view of them (runtime.cu:989-999, core.py:462-471);
+    here torch.matmul (hipBLASLt) on an fp16 copy decoded once, outside the
+    timed region."""
     import torch
 
     from mlbricks_amd.elasticbit import _native as native
@@ -276,20 +364,25 @@ def reference_route(args) -> dict:
     layer = compressed_layer(prows, pcols, 0.01, 512)
     nm = layer.matrix._native
     xp = torch.randn(M, pcols, generator=torch.Generator().manual_seed(1)).half().cuda()
-    wbuf = torch.empty(prows, pcols, dtype=torch.float16, device="cuda")
     yp = torch.empty(M, prows, dtype=torch.float16, device="cuda")
+    if nm.storageBits >= 9:
+        resident = nm._materializeTorch()          # decoded once, outside the timed region
+        ms = time_graph([lambda: torch.matmul(xp, resident.t(), out=yp)], args.prefill_steps, 3)
+        what = ("configs[3] as the reference runs it at b = 9..15: torch.matmul (hipBLASLt) on resident fp16 "
+                "weights (runtime.cu:989-999)")
+    else:
+        wbuf = torch.empty(prows, pcols, dtype=torch.float16, device="cuda")
 
-    def materialize_then_linear():
-        native.check(native.lib().eb_materialize_fp16(nm._h, wbuf.data_ptr(), native.stream_handle(wbuf.device)))
-        torch.matmul(xp, wbuf.t(), out=yp)
+        def materialize_then_linear():
+            native.check(native.lib().eb_materialize_fp16(nm._h, wbuf.data_ptr(), native.stream_handle(wbuf.device)))
+            torch.matmul(xp, wbuf.t(), out=yp)
 
-    ms = time_graph([materialize_then_linear], args.prefill_steps, 3)
+        ms = time_graph([materialize_then_linear], args.prefill_steps, 3)
+        what = "configs[3] as the reference runs it at b <= 8: materialize to fp16, then torch.matmul"
     us = ms / args.prefill_steps * 1e3
     flops = 2.0 * M * prows * pcols
-    out["prefill_materialize_then_linear"] = {
-        "us_per_launch": round(us, 2), "tflops": round(flops / (us * 1e-6) / 1e12, 1),
-        "what": "configs[3]: materialize_kernel to fp16, then torch.matmul (hipBLASLt), as core.py:462-471"}
-    log(f"reference route, prefill materialize + F.linear: {us:.1f} us/launch")
+    out["prefill"] = {"us_per_launch": round(us, 2), "tflops": round(flops / (us * 1e-6) / 1e12, 1), "what": what}
+    log(f"reference route, prefill: {us:.1f} us/launch ({what})")
     return out
 
 
@@ -299,7 +392,10 @@ def all_configs(args) -> int:
     the launch stream, weight copies rotated past the MALL for M <= 16),
     beside the reference's execution format on the same weights: W16A16
     decode for M = 1 at b = 9..15 (this build's GEMV over fp16 storage), and
-    materialize + F.linear (core.py:462-471) for M > 1."""
+    for M > 1 F.linear (core.py:462-471) on resident fp16 weights at
+    b = 9..15 (runtime.cu:989-999) or on weights materialized per call at
+    b <= 8 (runtime.cu:1001-1021).  Where our launches rotate over weight
+    copies, so do the reference's (fp16 copies)."""
     import torch
 
     from mlbricks_amd.elasticbit import _native as native
@@ -338,8 +434,13 @@ def all_configs(args) -> int:
             return ms / steps * 1e3, "W16A16 GEMV"
         if M == 1:
             return None, "W4/W8 GEMV (not timed)"
-        wbuf = torch.empty(rows, cols, dtype=torch.float16, device="cuda")
         y = torch.empty(M, rows, dtype=torch.float16, device="cuda")
+        if nm.storageBits >= 9:
+            keep = mats[: max(1, min(len(mats), -(-2 * MALL_BYTES // (2 * rows * cols)) + 1))]
+            w16s = [m._materializeTorch() for m in keep]      # resident, decoded outside the timing
+            ms = time_graph([lambda w=w: torch.matmul(x, w.t(), out=y) for w in w16s], steps, steps // 10)
+            return ms / steps * 1e3, "resident fp16 + F.linear"
+        wbuf = torch.empty(rows, cols, dtype=torch.float16, device="cuda")
 
         def mk(m):
             def run():
@@ -514,7 +615,9 @@ def m_sweep(args) -> int:
 
 def cpu_baseline(layer, seconds: float) -> dict:
     """The oracle's OpenMP GEMV (fp32 accumulate) over the same matrix and the
-    same algorithmic bytes, on this host's cores (bounded to ~`seconds`)."""
+    same algorithmic bytes, on every core this process may use (bounded to
+    ~`seconds`); beside it torch's fp32 F.linear on the CPU over the decoded
+    weights (BASELINE.md's secondary baseline)."""
     import numpy as np
     import torch
 
@@ -525,7 +628,7 @@ def cpu_baseline(layer, seconds: float) -> dict:
     scales, payload = nm._canonical()
     x16 = torch.randn(1, cols, generator=torch.Generator().manual_seed(1)).half().numpy().view(np.uint16)
     cores = len(os.sched_getaffinity(0))
-    threads = min(cores, 16)
+    threads = cores
     ora.gemv_f32_baseline(payload, scales, rows, cols, bits, x16, threads=threads)   # warm-up
     reps = 0
     t0 = time.perf_counter()
@@ -536,11 +639,27 @@ def cpu_baseline(layer, seconds: float) -> dict:
         if elapsed >= seconds:
             break
     per = elapsed / reps
-    gbs = algorithmic_bytes(rows, cols, bits, 1) / per / 1e9
+    nbytes = algorithmic_bytes(rows, cols, bits, 1)
+    gbs = nbytes / per / 1e9
     log(f"cpu baseline: {per * 1e3:.2f} ms/GEMV on {used} threads ({cores} cores visible): {gbs:.2f} GB/s")
+    # torch's fp32 F.linear over the decoded weights (the bytes are still
+    # counted at the storage width, as for every line of this benchmark)
+    wf = torch.from_numpy(np.asarray(ora.dequantize(payload, scales, rows, cols, bits)[0]))
+    xf = torch.from_numpy(x16.view(np.float16).astype(np.float32))
+    torch.nn.functional.linear(xf, wf)
+    treps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds / 2:
+        torch.nn.functional.linear(xf, wf)
+        treps += 1
+    tper = (time.perf_counter() - t0) / treps
+    log(f"cpu torch fp32 F.linear: {tper * 1e3:.2f} ms on {torch.get_num_threads()} threads")
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": int(used), "kind": "port",
             "sample": f"{reps} full 4096x4096 b={bits} M=1 GEMVs ({elapsed:.1f} s), oracle/eb_oracle.c "
-                      f"ebo_gemv_f32_baseline, OpenMP over rows; {cores} cores visible"}
+                      f"ebo_gemv_f32_baseline, OpenMP over rows; {cores} cores visible",
+            "torch_fp32_linear": {"value": round(nbytes / tper / 1e9, 3), "unit": "GB/s",
+                                  "threads": int(torch.get_num_threads()), "ms_per_call": round(tper * 1e3, 3),
+                                  "sample": f"{treps} calls of torch.nn.functional.linear(x.float(), W_decoded_f32) "
+                                            "on the CPU"}}
 
 
 def traffic_probe(args) -> int:
@@ -691,6 +810,9 @@ def main() -> int:
         return summarize_pmc(*args.summarize_pmc)
     if args.summarize_trace:
         return summarize_trace(args.summarize_trace)
+    if args.build_probe:
+        print(build_probe(force=True))
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the ElasticBit path is "
               "benchmarked on a single MI355X.", file=sys.stderr)
@@ -706,6 +828,8 @@ def main() -> int:
         return traffic_probe(args)
     if args.all_configs:
         return all_configs(args)
+    if args.ceiling_curve:
+        return ceiling_curve(args)
     if args.m_sweep:
         return m_sweep(args)
     if args.bolt_decode:

@@ -1,4 +1,5 @@
-// Read-bandwidth probe for bench.py (not part of the ElasticBit library).
+// Read-bandwidth probe for bench.py (not part of the ElasticBit library;
+// bench.py builds it on first use into _build/libeb_probe_read.so).
 //
 // Measures what a kernel that only reads a buffer of a given size achieves
 // when launched the way bench.py launches the GEMV: the same bytes, the same
@@ -7,16 +8,19 @@
 // the GEMV's HBM fraction is then read against.
 //
 // Each workgroup reads one contiguous chunk; every thread issues all of its
-// 16-byte loads before it uses any.  The XOR of the data is written only if
-// it equals a value it never takes, so the loads stay live and nothing is
-// stored.
+// 16-byte loads before it uses any (up to 32 per thread, 512 bytes in
+// flight), optionally as nontemporal loads.  The XOR of the data is written
+// only if it equals a value it never takes, so the loads stay live and
+// nothing is stored.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
 
 namespace {
 
-template <int T, int L>
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+template <int T, int L, bool NT>
 __global__ __launch_bounds__(T) void read_chunks(const uint4* __restrict__ src, uint64_t n16, uint64_t chunk16,
                                                   uint32_t* __restrict__ sink) {
     const uint64_t base = static_cast<uint64_t>(blockIdx.x) * chunk16;
@@ -24,7 +28,16 @@ __global__ __launch_bounds__(T) void read_chunks(const uint4* __restrict__ src, 
 #pragma unroll
     for (int i = 0; i < L; ++i) {
         const uint64_t idx = threadIdx.x + static_cast<uint64_t>(i) * T;
-        v[i] = (idx < chunk16 && base + idx < n16) ? src[base + idx] : make_uint4(0, 0, 0, 0);
+        if (idx < chunk16 && base + idx < n16) {
+            if constexpr (NT) {
+                const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src) + base + idx);
+                v[i] = make_uint4(w.x, w.y, w.z, w.w);
+            } else {
+                v[i] = src[base + idx];
+            }
+        } else {
+            v[i] = make_uint4(0, 0, 0, 0);
+        }
     }
     uint32_t acc = 0;
 #pragma unroll
@@ -32,37 +45,48 @@ __global__ __launch_bounds__(T) void read_chunks(const uint4* __restrict__ src, 
     if (acc == 0x9E3779B9u && threadIdx.x == 0) sink[blockIdx.x & 1023] = acc;
 }
 
-template <int T>
+template <int T, bool NT>
 int launch(const uint4* src, uint64_t n16, int blocks, uint32_t* sink, hipStream_t s) {
     const uint64_t chunk16 = (n16 + blocks - 1) / blocks;
-    if (chunk16 <= static_cast<uint64_t>(T) * 2) {
-        hipLaunchKernelGGL((read_chunks<T, 2>), dim3(blocks), dim3(T), 0, s, src, n16, chunk16, sink);
-    } else if (chunk16 <= static_cast<uint64_t>(T) * 4) {
-        hipLaunchKernelGGL((read_chunks<T, 4>), dim3(blocks), dim3(T), 0, s, src, n16, chunk16, sink);
-    } else if (chunk16 <= static_cast<uint64_t>(T) * 8) {
-        hipLaunchKernelGGL((read_chunks<T, 8>), dim3(blocks), dim3(T), 0, s, src, n16, chunk16, sink);
-    } else if (chunk16 <= static_cast<uint64_t>(T) * 16) {
-        hipLaunchKernelGGL((read_chunks<T, 16>), dim3(blocks), dim3(T), 0, s, src, n16, chunk16, sink);
+    const uint64_t per = (chunk16 + T - 1) / T;     // 16-byte loads per thread
+    if (per <= 2) {
+        hipLaunchKernelGGL((read_chunks<T, 2, NT>), dim3(blocks), dim3(T), 0, s, src, n16, chunk16, sink);
+    } else if (per <= 4) {
+        hipLaunchKernelGGL((read_chunks<T, 4, NT>), dim3(blocks), dim3(T), 0, s, src, n16, chunk16, sink);
+    } else if (per <= 8) {
+        hipLaunchKernelGGL((read_chunks<T, 8, NT>), dim3(blocks), dim3(T), 0, s, src, n16, chunk16, sink);
+    } else if (per <= 16) {
+        hipLaunchKernelGGL((read_chunks<T, 16, NT>), dim3(blocks), dim3(T), 0, s, src, n16, chunk16, sink);
+    } else if (per <= 32) {
+        hipLaunchKernelGGL((read_chunks<T, 32, NT>), dim3(blocks), dim3(T), 0, s, src, n16, chunk16, sink);
     } else {
         return -1;   // too many bytes per thread for this launch shape
     }
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
+template <bool NT>
+int launch_threads(const uint4* src, uint64_t n16, int blocks, int threads, uint32_t* sink, hipStream_t s) {
+    switch (threads) {
+        case 256: return launch<256, NT>(src, n16, blocks, sink, s);
+        case 512: return launch<512, NT>(src, n16, blocks, sink, s);
+        case 1024: return launch<1024, NT>(src, n16, blocks, sink, s);
+        default: return -1;
+    }
+}
+
 }  // namespace
 
 // Read `bytes` (a multiple of 16) from `src` with `blocks` workgroups of
-// `threads` (256, 512 or 1024) threads; `sink` is a device buffer of 1024
-// uint32.  0 on success, -1 for an unsupported shape, -2 on a launch error.
-extern "C" int eb_probe_read(const void* src, uint64_t bytes, int blocks, int threads, void* sink, void* stream) {
+// `threads` (256, 512 or 1024) threads, with nontemporal loads when
+// `nontemporal` is nonzero; `sink` is a device buffer of 1024 uint32.  0 on
+// success, -1 for an unsupported shape, -2 on a launch error.
+extern "C" int eb_probe_read(const void* src, uint64_t bytes, int blocks, int threads, int nontemporal, void* sink,
+                             void* stream) {
     if (!src || !sink || bytes % 16 != 0 || blocks <= 0) return -1;
     const auto* s16 = static_cast<const uint4*>(src);
     auto* out = static_cast<uint32_t*>(sink);
     const auto st = static_cast<hipStream_t>(stream);
-    switch (threads) {
-        case 256: return launch<256>(s16, bytes / 16, blocks, out, st);
-        case 512: return launch<512>(s16, bytes / 16, blocks, out, st);
-        case 1024: return launch<1024>(s16, bytes / 16, blocks, out, st);
-        default: return -1;
-    }
+    return nontemporal ? launch_threads<true>(s16, bytes / 16, blocks, threads, out, st)
+                       : launch_threads<false>(s16, bytes / 16, blocks, threads, out, st);
 }
