@@ -171,9 +171,13 @@ def time_graph(launches, steps: int, warmup: int) -> float:
     once untimed, then once between HIP events on the launch stream.  Returns ms.
 
     Before the timed replay a spin kernel holds the stream for 1 ms plus 10 us
-    per step, so the host has queued the whole replay before the start event
-    executes: the events bracket exactly `steps` launches running back to
-    back, whatever `steps` is, and the host's enqueue cost stays outside."""
+    per step, so the host has queued everything after it before the start
+    event executes; between the spin and the start event run untimed
+    launches of the same steps (the replay of a warm-up graph of at least
+    `warmup` launches and 2 ms of work), so the GPU is at its working clock
+    and the launches' page-table entries are warm.  The events then bracket
+    exactly `steps` launches running back to back, whatever `steps` is, and
+    the host's enqueue cost stays outside."""
     import torch
 
     for i in range(warmup):
@@ -187,13 +191,28 @@ def time_graph(launches, steps: int, warmup: int) -> float:
             for i in range(steps):
                 launches[i % len(launches)]()
     torch.cuda.synchronize()
-    graph.replay()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        t0.record(stream)
+        graph.replay()
+        t1.record(stream)
+    t1.synchronize()
+    per_launch_ms = max(float(t0.elapsed_time(t1)) / steps, 1e-4)
+    # warm-up graph: the same launches, at least `warmup` of them and ~2 ms
+    warm_n = max(warmup, min(20000, int(2.0 / per_launch_ms) + 1))
+    warm = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(warm, stream=stream):
+            for i in range(warm_n):
+                launches[(i - warm_n) % len(launches)]()
     torch.cuda.synchronize()
-    hold = int(_spin_cycles_per_ms() * (1.0 + 0.01 * steps))
+    hold = int(_spin_cycles_per_ms() * (1.0 + 0.01 * (steps + warm_n)))
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
         torch.cuda._sleep(hold)
+        warm.replay()
         start.record(stream)
         graph.replay()
         stop.record(stream)
@@ -859,7 +878,8 @@ def main() -> int:
             "storage_bits": g["bits"],
             "weight_copies_rotated": g["copies"],
             "bytes_per_step": g["bytes"],
-            "timing": "one HIP graph of `steps` launches, HIP events on the launch stream",
+            "timing": "HIP events on the launch stream around one graph replay of exactly `steps` launches, "
+                      "queued behind a spin kernel and >= 2 ms of untimed warm launches",
         },
         "roofline": {
             "bound": "hbm",

@@ -560,7 +560,9 @@ class RuntimeMatrix:
         shape = (*x.shape[:-1], p.rows)
         if out is None:
             out = torch.empty(shape, dtype=torch.float16, device=x.device)
-        elif out.dtype != torch.float16 or not out.is_contiguous() or out.numel() != m * p.rows:
+        elif not (out.is_cuda and out.device == x.device):
+            raise ValueError("out must be on the input's device")
+        elif out.dtype != torch.float16 or not out.is_contiguous() or tuple(out.shape) != shape:
             raise ValueError("out must be a contiguous fp16 tensor of the output shape")
         b = None
         if bias is not None:

@@ -751,3 +751,22 @@ def test_multi_matrix_decode_over_large_matrices(native, M):
     ys = native.forward_torch_multi(mats, x, biases)
     for j, (mm, yj) in enumerate(zip(mats, ys)):
         assert torch.equal(yj, mm.forwardTorch(x, bias=biases[j])), j
+
+
+def test_forward_rejects_out_on_another_device_or_of_another_shape(native):
+    """A caller-supplied ``out`` must be fp16, contiguous, on the input's device
+    and of the output's exact shape; every rejection happens before a launch."""
+    rng = np.random.default_rng(4)
+    m = native.RuntimeMatrix._compressSelectedCodes(_codes(rng, 64, 128, 8), np.ones(64, np.float32), 8, 0.01, 0.0)
+    x = _x16(rng, 2, 128)
+    with pytest.raises(ValueError, match="input's device"):
+        m.forwardTorch(x, out=torch.empty(2, 64, dtype=torch.float16))
+    with pytest.raises(ValueError, match="output shape"):
+        m.forwardTorch(x, out=torch.empty(128, dtype=torch.float16, device="cuda"))
+    with pytest.raises(ValueError, match="output shape"):
+        m.forwardTorch(x, out=torch.empty(2, 64, dtype=torch.float32, device="cuda"))
+    with pytest.raises(ValueError, match="output shape"):
+        m.forwardTorch(x, out=torch.empty(64, 2, dtype=torch.float16, device="cuda").t())
+    y = torch.empty(2, 64, dtype=torch.float16, device="cuda")
+    assert m.forwardTorch(x, out=y) is y
+    assert torch.equal(y, m.forwardTorch(x))
