@@ -7,8 +7,8 @@ fp16 activations M=1, weights N(0,0.02) with 1% x8 outlier columns, compressed
 by ElasticBit.compress at threshold 0.01 (the GPU width search picks b).  One
 step is one fused unpack+dequant+GEMV launch over one weight copy; the copies
 rotate over >= 512 MB so the 256 MB MALL cannot hold them, and the K steps are
-captured into one HIP graph and replayed, timed with HIP events on the stream
-the kernels run on.  value = algorithmic bytes per step / time per step, with
+queued behind a spin kernel and timed with HIP events on the stream the
+kernels run on.  value = algorithmic bytes per step / time per step, with
 bytes counted at the storage width: ceil(N*K*b/8) + 4N + 2MK + 2MN.
 
 Also reported (not the headline): the prefill GEMM of configs[3] (4096->14336,
@@ -36,6 +36,8 @@ Profiling helpers (same file, so the committed summaries name committed code):
     python bench.py --traffic-probe      # eager launches for rocprofv3 --pmc passes
     python bench.py --summarize-pmc FETCH.csv WRITE.csv    # -> profiles/*_traffic.md
     python bench.py --summarize-trace KERNEL_STATS.csv     # -> kernel table (markdown)
+    python bench.py --counter-probe      # eager decode / prefill / hipBLASLt launches for counter passes
+    python bench.py --summarize-counters A.csv B.csv C.csv  # -> per-kernel counter table (markdown)
 """
 from __future__ import annotations
 
@@ -84,6 +86,10 @@ def parse_args() -> argparse.Namespace:
                    help="run eager GEMV/prefill launches and a calibration copy for rocprofv3 --pmc")
     p.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
     p.add_argument("--summarize-trace", metavar="KERNEL_STATS_CSV")
+    p.add_argument("--counter-probe", action="store_true",
+                   help="eager launches for rocprofv3 --pmc counter passes: the configs[1] GEMV, configs[3] "
+                        "through both 256 x 256 prefill kernels, and hipBLASLt on resident fp16 weights")
+    p.add_argument("--summarize-counters", nargs="+", metavar="COUNTER_CSV")
     p.add_argument("--bolt-decode", action="store_true",
                    help="configs[4]'s compressed Linears: one greedy decode token's 96 M = 1 forwards "
                         "(12 layers) plus the tied fp16 LM head, timed per token")
@@ -166,59 +172,53 @@ def _spin_cycles_per_ms() -> float:
     return _SPIN_CYCLES_PER_MS
 
 
-def time_graph(launches, steps: int, warmup: int) -> float:
-    """Capture `steps` launches (cycling over `launches`) into one HIP graph, replay it
-    once untimed, then once between HIP events on the launch stream.  Returns ms.
+def time_launches(launches, steps: int, warmup: int) -> float:
+    """Time exactly `steps` launches (cycling over `launches`) with HIP events
+    on the launch stream.  Returns ms.
 
-    Before the timed replay a spin kernel holds the stream for 1 ms plus 10 us
-    per step, so the host has queued everything after it before the start
-    event executes; between the spin and the start event run untimed
-    launches of the same steps (the replay of a warm-up graph of at least
-    `warmup` launches and 2 ms of work), so the GPU is at its working clock
-    and the launches' page-table entries are warm.  The events then bracket
-    exactly `steps` launches running back to back, whatever `steps` is, and
-    the host's enqueue cost stays outside."""
+    A spin kernel first holds the stream long enough for the host to queue
+    everything after it: `warmup` untimed launches (and more, up to ~2 ms of
+    work, so the GPU runs at its working clock), the start event, the
+    `steps` timed launches and the stop event.  The events then bracket
+    exactly `steps` launches running back to back, and the host's enqueue
+    cost stays outside whatever `steps` is.  (A captured graph replay was
+    measured to add ~4 us of device-side start-up per replay, which a short
+    run would charge to its few steps; eager launches behind the spin do
+    not.)"""
     import torch
 
-    for i in range(warmup):
-        launches[i % len(launches)]()
-    torch.cuda.synchronize()
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
-    graph = torch.cuda.CUDAGraph()
     with torch.cuda.stream(stream):
-        with torch.cuda.graph(graph, stream=stream):
-            for i in range(steps):
-                launches[i % len(launches)]()
-    torch.cuda.synchronize()
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(stream):
-        t0.record(stream)
-        graph.replay()
-        t1.record(stream)
-    t1.synchronize()
-    per_launch_ms = max(float(t0.elapsed_time(t1)) / steps, 1e-4)
-    # warm-up graph: the same launches, at least `warmup` of them and ~2 ms
-    warm_n = max(warmup, min(20000, int(2.0 / per_launch_ms) + 1))
-    warm = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(stream):
-        with torch.cuda.graph(warm, stream=stream):
+        for i in range(max(1, warmup)):
+            launches[i % len(launches)]()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(min(steps, 50)):
+            launches[i % len(launches)]()
+        torch.cuda.synchronize()
+        per_launch_ms = max((time.perf_counter() - t0) * 1e3 / min(steps, 50), 1e-4)
+    warm_n = max(warmup, min(5000, int(2.0 / per_launch_ms) + 1))
+    hold_ms = 2.0
+    for _ in range(6):
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            t_host = time.perf_counter()
+            torch.cuda._sleep(int(_spin_cycles_per_ms() * hold_ms))
             for i in range(warm_n):
                 launches[(i - warm_n) % len(launches)]()
-    torch.cuda.synchronize()
-    hold = int(_spin_cycles_per_ms() * (1.0 + 0.01 * (steps + warm_n)))
-    start = torch.cuda.Event(enable_timing=True)
-    stop = torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(stream):
-        torch.cuda._sleep(hold)
-        warm.replay()
-        start.record(stream)
-        graph.replay()
-        stop.record(stream)
-    stop.synchronize()
-    torch.cuda.synchronize()
-    return float(start.elapsed_time(stop))
+            start.record(stream)
+            for i in range(steps):
+                launches[i % len(launches)]()
+            stop.record(stream)
+            enqueue_ms = (time.perf_counter() - t_host) * 1e3
+        stop.synchronize()
+        torch.cuda.synchronize()
+        if enqueue_ms < 0.8 * hold_ms:
+            return float(start.elapsed_time(stop))
+        hold_ms = 2.0 * enqueue_ms          # the host was slower than the spin: hold longer
+    raise RuntimeError("could not queue the timed launches ahead of the GPU")
 
 
 def bench_gemv(args) -> dict:
@@ -234,7 +234,7 @@ def bench_gemv(args) -> dict:
     x = torch.randn(1, cols, generator=torch.Generator().manual_seed(1)).half().cuda()
     outs = [torch.empty(1, rows, dtype=torch.float16, device="cuda") for _ in mats]
     launches = [lambda m=m, y=y: m.forwardTorch(x, out=y) for m, y in zip(mats, outs)]
-    ms = time_graph(launches, args.steps, args.warmup)
+    ms = time_launches(launches, args.steps, args.warmup)
     per_step_ms = ms / args.steps
     nbytes = algorithmic_bytes(rows, cols, bits, 1)
     gbs = nbytes / (per_step_ms * 1e-3) / 1e9
@@ -252,7 +252,7 @@ def bench_prefill(args) -> dict:
     x = torch.randn(M, cols, generator=torch.Generator().manual_seed(1)).half().cuda()
     y = torch.empty(M, rows, dtype=torch.float16, device="cuda")
     nm = layer.matrix._native
-    ms = time_graph([lambda: nm.forwardTorch(x, out=y)], args.prefill_steps, 3)
+    ms = time_launches([lambda: nm.forwardTorch(x, out=y)], args.prefill_steps, 3)
     per = ms / args.prefill_steps
     flops = 2.0 * M * rows * cols
     tflops = flops / (per * 1e-3) / 1e12
@@ -315,7 +315,7 @@ def read_ceiling(nbytes: int, copies: int, steps: int, warmup: int) -> dict:
                     raise RuntimeError(f"eb_probe_read: {rc}")
             return launch
         try:
-            ms = time_graph([mk(b) for b in bufs], steps, warmup)
+            ms = time_launches([mk(b) for b in bufs], steps, warmup)
         except RuntimeError:
             continue
         us = ms / steps * 1e3
@@ -329,7 +329,7 @@ def read_ceiling(nbytes: int, copies: int, steps: int, warmup: int) -> dict:
     return {"us_per_launch": round(us, 3), "gbs": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
             "launch": f"{blocks} workgroups x {threads} threads, {kind} loads",
             "what": "pure-read kernel (probe_read.hip) over the GEMV's algorithmic bytes, "
-                    "same copy rotation and graph timing"}
+                    "same copy rotation and timing"}
 
 
 def ceiling_curve(args) -> int:
@@ -370,7 +370,7 @@ def reference_route(args) -> dict:
     mats = [native.RuntimeMatrix._compressSelected(w, 16, 0.01, 0.0) for _ in range(n_copies)]
     x = torch.randn(1, cols, generator=torch.Generator().manual_seed(1)).half().cuda()
     ys = [torch.empty(1, rows, dtype=torch.float16, device="cuda") for _ in mats]
-    ms = time_graph([lambda m=m, y=y: m.forwardTorch(x, out=y) for m, y in zip(mats, ys)], args.steps, args.warmup)
+    ms = time_launches([lambda m=m, y=y: m.forwardTorch(x, out=y) for m, y in zip(mats, ys)], args.steps, args.warmup)
     us = ms / args.steps * 1e3
     nbytes = algorithmic_bytes(rows, cols, 16, 1)
     out["decode_w16"] = {"us_per_launch": round(us, 3), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
@@ -386,7 +386,7 @@ def reference_route(args) -> dict:
     yp = torch.empty(M, prows, dtype=torch.float16, device="cuda")
     if nm.storageBits >= 9:
         resident = nm._materializeTorch()          # decoded once, outside the timed region
-        ms = time_graph([lambda: torch.matmul(xp, resident.t(), out=yp)], args.prefill_steps, 3)
+        ms = time_launches([lambda: torch.matmul(xp, resident.t(), out=yp)], args.prefill_steps, 3)
         what = ("configs[3] as the reference runs it at b = 9..15: torch.matmul (hipBLASLt) on resident fp16 "
                 "weights (runtime.cu:989-999)")
     else:
@@ -396,7 +396,7 @@ def reference_route(args) -> dict:
             native.check(native.lib().eb_materialize_fp16(nm._h, wbuf.data_ptr(), native.stream_handle(wbuf.device)))
             torch.matmul(xp, wbuf.t(), out=yp)
 
-        ms = time_graph([materialize_then_linear], args.prefill_steps, 3)
+        ms = time_launches([materialize_then_linear], args.prefill_steps, 3)
         what = "configs[3] as the reference runs it at b <= 8: materialize to fp16, then torch.matmul"
     us = ms / args.prefill_steps * 1e3
     flops = 2.0 * M * prows * pcols
@@ -407,7 +407,7 @@ def reference_route(args) -> dict:
 
 def all_configs(args) -> int:
     """Every BASELINE configuration that runs on one GPU, compressed by the
-    real ElasticBit.compress, timed like the headline (HIP graph, events on
+    real ElasticBit.compress, timed like the headline (spin-held launches, events on
     the launch stream, weight copies rotated past the MALL for M <= 16),
     beside the reference's execution format on the same weights: W16A16
     decode for M = 1 at b = 9..15 (this build's GEMV over fp16 storage), and
@@ -438,7 +438,7 @@ def all_configs(args) -> int:
         cols, rows = mats[0].cols, mats[0].rows
         x = torch.randn(M, cols, generator=torch.Generator().manual_seed(1)).half().cuda()
         ys = [torch.empty(M, rows, dtype=torch.float16, device="cuda") for _ in mats]
-        ms = time_graph([lambda m=m, y=y: m.forwardTorch(x, out=y) for m, y in zip(mats, ys)], steps, steps // 10)
+        ms = time_launches([lambda m=m, y=y: m.forwardTorch(x, out=y) for m, y in zip(mats, ys)], steps, steps // 10)
         return ms / steps * 1e3
 
     def reference(mats, M, steps):
@@ -449,7 +449,7 @@ def all_configs(args) -> int:
             w16 = [native.RuntimeMatrix._compressSelected(m._materializeTorch().float().cpu().numpy(), 16, 0.01, 0.0)
                    for m in mats[: max(2, -(-2 * MALL_BYTES // (2 * rows * cols)) + 1)]]
             ys = [torch.empty(1, rows, dtype=torch.float16, device="cuda") for _ in w16]
-            ms = time_graph([lambda m=m, y=y: m.forwardTorch(x, out=y) for m, y in zip(w16, ys)], steps, steps // 10)
+            ms = time_launches([lambda m=m, y=y: m.forwardTorch(x, out=y) for m, y in zip(w16, ys)], steps, steps // 10)
             return ms / steps * 1e3, "W16A16 GEMV"
         if M == 1:
             return None, "W4/W8 GEMV (not timed)"
@@ -457,7 +457,7 @@ def all_configs(args) -> int:
         if nm.storageBits >= 9:
             keep = mats[: max(1, min(len(mats), -(-2 * MALL_BYTES // (2 * rows * cols)) + 1))]
             w16s = [m._materializeTorch() for m in keep]      # resident, decoded outside the timing
-            ms = time_graph([lambda w=w: torch.matmul(x, w.t(), out=y) for w in w16s], steps, steps // 10)
+            ms = time_launches([lambda w=w: torch.matmul(x, w.t(), out=y) for w in w16s], steps, steps // 10)
             return ms / steps * 1e3, "resident fp16 + F.linear"
         wbuf = torch.empty(rows, cols, dtype=torch.float16, device="cuda")
 
@@ -466,7 +466,7 @@ def all_configs(args) -> int:
                 native.check(native.lib().eb_materialize_fp16(m._h, wbuf.data_ptr(), native.stream_handle(wbuf.device)))
                 torch.matmul(x, wbuf.t(), out=y)
             return run
-        ms = time_graph([mk(m) for m in mats], steps, steps // 10)
+        ms = time_launches([mk(m) for m in mats], steps, steps // 10)
         return ms / steps * 1e3, "materialize + F.linear"
 
     lines = ["| config | N x K | thr | b | M | ours us | GB/s (% HBM) | TFLOP/s (% fp16) | reference route | ref us |",
@@ -518,7 +518,7 @@ def bolt_decode(args) -> int:
     ceiling set by the Linears alone.  Weights: nn.Linear's default init
     under seed 0 (head_gate zero), compressed by ElasticBit.compress at
     threshold 0.01 with 32 seeded N(0,1) calibration rows per Linear.  The
-    timed graph replays whole tokens back to back, as a decode loop does, so
+    timed launches run whole tokens back to back, as a decode loop does, so
     whatever of the model fits in the MALL stays there as it would in a real
     run."""
     import torch
@@ -578,7 +578,7 @@ def bolt_decode(args) -> int:
     for label, fn in (("96 Linears + LM head", token_separate),
                       ("q/k/v/head_gate fused + LM head", token_fused),
                       ("LM head alone", head_only)):
-        us = time_graph([fn], tokens, 3) / tokens * 1e3
+        us = time_launches([fn], tokens, 3) / tokens * 1e3
         rows.append((label, us))
         log(f"  {label}: {us:.1f} us per token")
     head_us = rows[2][1]
@@ -623,7 +623,7 @@ def m_sweep(args) -> int:
             x = torch.randn(M, cols, generator=torch.Generator().manual_seed(1)).half().cuda()
             ys = [torch.empty(M, rows, dtype=torch.float16, device="cuda") for _ in mats]
             steps = 400 if M <= 64 else max(40, len(mats))
-            ms = time_graph([lambda m=m, y=y: m.forwardTorch(x, out=y) for m, y in zip(mats, ys)], steps, 3)
+            ms = time_launches([lambda m=m, y=y: m.forwardTorch(x, out=y) for m, y in zip(mats, ys)], steps, 3)
             cells.append(f"{ms / steps * 1e3:.1f}")
         lines.append(f"| {rows} x {cols} | " + " | ".join(cells) + " |")
         log(lines[-1])
@@ -710,6 +710,91 @@ def traffic_probe(args) -> int:
             big.matrix._native.forwardTorch(xp, out=yp)
         torch.cuda.synchronize()
         log(f"probe: 4 prefill launches, b={big.matrix.storageBits}")
+    return 0
+
+
+def counter_probe(args) -> int:
+    """Eager launches whose counters `--summarize-counters` compares: the
+    headline GEMV, configs[3] through the eight-wave and the
+    four-wave 256 x 256 prefill kernels, and torch.matmul (hipBLASLt) on
+    the same weights decoded to resident fp16 (the reference's route)."""
+    import torch
+
+    from mlbricks_amd.elasticbit import _native as native
+
+    layer = compressed_layer(4096, 4096, 0.01, 512)
+    mats = copies_of(layer, max(2, -(-2 * MALL_BYTES // layer.matrix.executionBytes) + 1))
+    x = torch.randn(1, 4096, generator=torch.Generator().manual_seed(1)).half().cuda()
+    y = torch.empty(1, 4096, dtype=torch.float16, device="cuda")
+    for i in range(args.steps):
+        mats[i % len(mats)].forwardTorch(x, out=y)
+    torch.cuda.synchronize()
+    log(f"probe: {args.steps} GEMV launches")
+    big = compressed_layer(14336, 4096, 0.01, 512).matrix._native
+    xp = torch.randn(2048, 4096, generator=torch.Generator().manual_seed(1)).half().cuda()
+    yp = torch.empty(2048, 14336, dtype=torch.float16, device="cuda")
+    for mode in ("wide8", "wide"):
+        native.set_prefill_tiles(mode)
+        for _ in range(4):
+            big.forwardTorch(xp, out=yp)
+        torch.cuda.synchronize()
+        log(f"probe: 4 prefill launches, {mode} tiles, b={big.storageBits}")
+    native.set_prefill_tiles("auto")
+    resident = big._materializeTorch()
+    for _ in range(4):
+        torch.matmul(xp, resident.t(), out=yp)
+    torch.cuda.synchronize()
+    log("probe: 4 torch.matmul launches on resident fp16")
+    return 0
+
+
+def summarize_counters(paths: list[str]) -> int:
+    """Per-kernel averages of counter passes over `--counter-probe` (first
+    dispatch of each kernel dropped as warm-up), with the clock (GRBM_GUI_ACTIVE
+    per XCD over the dispatch's duration) and the MFMA-busy fraction of the
+    SIMDs over those cycles."""
+    import collections
+    import csv
+    import statistics
+
+    wanted = ("linear_gemv_kernel", "linear_prefill_pp_kernel", "linear_prefill_wide_kernel", "Cijk")
+    table: dict[str, dict[str, list[float]]] = collections.defaultdict(lambda: collections.defaultdict(list))
+    for path in paths:
+        per: dict[int, dict] = collections.defaultdict(dict)
+        for r in csv.DictReader(open(path, newline="")):
+            d = per[int(r["Dispatch_Id"])]
+            d["name"] = r["Kernel_Name"]
+            d[r["Counter_Name"]] = float(r["Counter_Value"])
+            d["duration_us"] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        seen = collections.Counter()
+        for did in sorted(per):
+            d = per[did]
+            key = next((w for w in wanted if w in d["name"]), None)
+            if key is None:
+                continue
+            seen[key] += 1
+            if seen[key] == 1:
+                continue                      # warm-up dispatch
+            for k, v in d.items():
+                if k != "name":
+                    table[key][k].append(v)
+    cols = sorted({k for t in table.values() for k in t if k not in ("duration_us",)})
+    lines = ["| kernel | dispatches | us | clock GHz | MFMA busy | " + " | ".join(cols) + " |",
+             "|---" * (len(cols) + 5) + "|"]
+    for key in wanted:
+        if key not in table:
+            continue
+        t = table[key]
+        avg = {k: statistics.mean(v) for k, v in t.items()}
+        n = max(len(v) for v in t.values())
+        grbm = avg.get("GRBM_GUI_ACTIVE", 0.0) / 8                  # eight XCDs
+        ghz = grbm / (avg["duration_us"] * 1e3) if grbm else float("nan")
+        busy = avg["SQ_VALU_MFMA_BUSY_CYCLES"] / (grbm * 1024) if grbm and "SQ_VALU_MFMA_BUSY_CYCLES" in avg \
+            else float("nan")
+        name = "hipBLASLt fp16 GEMM (resident weights)" if key == "Cijk" else key
+        lines.append(f"| `{name}` | {n} | {avg['duration_us']:.2f} | {ghz:.3f} | {busy:.3f} | "
+                     + " | ".join(f"{avg[c]:.4g}" if c in avg else "-" for c in cols) + " |")
+    print("\n".join(lines))
     return 0
 
 
@@ -832,6 +917,8 @@ def main() -> int:
     if args.build_probe:
         print(build_probe(force=True))
         return 0
+    if args.summarize_counters:
+        return summarize_counters(args.summarize_counters)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the ElasticBit path is "
               "benchmarked on a single MI355X.", file=sys.stderr)
@@ -845,6 +932,8 @@ def main() -> int:
 
     if args.traffic_probe:
         return traffic_probe(args)
+    if args.counter_probe:
+        return counter_probe(args)
     if args.all_configs:
         return all_configs(args)
     if args.ceiling_curve:
@@ -878,8 +967,8 @@ def main() -> int:
             "storage_bits": g["bits"],
             "weight_copies_rotated": g["copies"],
             "bytes_per_step": g["bytes"],
-            "timing": "HIP events on the launch stream around one graph replay of exactly `steps` launches, "
-                      "queued behind a spin kernel and >= 2 ms of untimed warm launches",
+            "timing": "HIP events on the launch stream around exactly `steps` launches, all queued behind a "
+                      "spin kernel and >= 2 ms of untimed warm launches",
         },
         "roofline": {
             "bound": "hbm",
