@@ -205,6 +205,19 @@ enum { EB_ANALYZE_TILE_ROWS = 16, EB_ANALYZE_MAX_SAMPLES = 32, EB_ANALYZE_SUMS =
 int eb_analyze_widths_device(const void* w_f16, int64_t rows, int64_t cols, const void* x_f16, int64_t samples,
                              const float* max_abs, float* partials, void* stream);
 
+/* No counterpart in the reference.  eb_analyze_widths_device for callers
+ * that cannot allocate (code under HIP graph capture, allocation-free
+ * compression or serving loops): the per-tile partial sums stay in a static
+ * device array of the library (1.5 MiB per device, held until the process
+ * ends), and totals [EB_ANALYZE_SUMS] (double, device, caller-owned) receives
+ * their sums over the tiles, added on the device in a fixed order.  At most
+ * EB_ANALYZE_STATIC_MAX_ROWS rows (EB_INVALID_ARGUMENT beyond).  Calls no
+ * allocator.  Every call on a device shares that device's array: calls that
+ * overlap on one device (concurrent streams) race.  Stream-ordered. */
+enum { EB_ANALYZE_STATIC_MAX_ROWS = 262144 };
+int eb_analyze_widths_device_totals(const void* w_f16, int64_t rows, int64_t cols, const void* x_f16,
+                                    int64_t samples, const float* max_abs, double* totals, void* stream);
+
 /* RuntimeMatrix._materializeTorch, runtime.cu:982-1022: out [rows][cols] fp16
  * = fp16_rn(q*s) (b = 16: the stored fp16). */
 int eb_materialize_fp16(const eb_matrix* m, void* out_f16, void* stream);

@@ -28,7 +28,16 @@
 
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 namespace ebk {
+
+// Per-tile partial sums of the width search that allocates nothing
+// (launch_analyze_widths_totals): one copy per device, as many tiles as
+// kAnalyzeScratchTiles.  Host code must not pass this name to a kernel (it is
+// a host-side stand-in); analyze_scratch() looks up its device address.
+static __device__ __align__(256) float scratch[kAnalyzeScratchTiles * kAnalyzeSums];
+
 namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -189,7 +198,55 @@ __global__ __launch_bounds__(64 * kAnWaves) void analyze_widths_kernel(
     }
 }
 
+// totals[j] = sum over tiles of partials[t][j] in double, in a fixed order
+// (lane l takes tiles l, l + 64, ...; then a shuffle tree): one wave per sum.
+__global__ __launch_bounds__(64) void analyze_total_kernel(const float* __restrict__ partials, int tiles,
+                                                           double* __restrict__ totals) {
+    const int lane = threadIdx.x;
+    const int j = blockIdx.x;
+    double v = 0.0;
+    for (int t = lane; t < tiles; t += 64) v += static_cast<double>(partials[static_cast<size_t>(t) * kAnalyzeSums + j]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    if (lane == 0) totals[j] = v;
+}
+
+// Device address of `scratch` on the current device, looked up once per
+// device with that device current and kept.
+hipError_t analyze_scratch(float** out) {
+    static std::mutex mu;
+    static float* per_device[64] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(mu);
+    if (per_device[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        per_device[dev] = static_cast<float*>(p);
+    }
+    *out = per_device[dev];
+    return hipSuccess;
+}
+
 }  // namespace
+
+hipError_t launch_analyze_widths_totals(const uint16_t* w, int N, int K, const uint16_t* x, int S,
+                                        const float* max_abs, double* totals, hipStream_t stream) {
+    const int tiles = (N + kAnRows - 1) / kAnRows;
+    if (N < 1 || tiles > kAnalyzeScratchTiles) return hipErrorInvalidValue;
+    float* partials = nullptr;
+    const hipError_t e = analyze_scratch(&partials);
+    if (e != hipSuccess) return e;
+    // every tile's sums are written by the first kernel before the second
+    // reads them, so nothing left by an earlier call needs clearing
+    const hipError_t e1 = launch_analyze_widths(w, N, K, x, S, max_abs, partials, stream);
+    if (e1 != hipSuccess) return e1;
+    hipLaunchKernelGGL(analyze_total_kernel, dim3(kAnalyzeSums), dim3(64), 0, stream, partials, tiles, totals);
+    return hipGetLastError();
+}
 
 hipError_t launch_analyze_widths(const uint16_t* w, int N, int K, const uint16_t* x, int S, const float* max_abs,
                                  float* partials, hipStream_t stream) {

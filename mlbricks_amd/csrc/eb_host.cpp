@@ -1047,6 +1047,25 @@ int eb_analyze_widths_device(const void* w_f16, int64_t rows, int64_t cols, cons
     });
 }
 
+int eb_analyze_widths_device_totals(const void* w_f16, int64_t rows, int64_t cols, const void* x_f16,
+                                    int64_t samples, const float* max_abs, double* totals, void* stream) {
+    return guarded([&] {
+        static_assert(EB_ANALYZE_STATIC_MAX_ROWS == ebk::kAnalyzeScratchTiles * ebk::kAnalyzeTileRows,
+                      "static scratch size");
+        require(w_f16 && x_f16 && max_abs && totals, "analyze_widths_totals: null pointer");
+        require(rows >= 1 && cols >= 1 && cols <= 0x7fffffffLL,
+                "analyze_widths_totals: rows and cols must be positive");
+        require(rows <= EB_ANALYZE_STATIC_MAX_ROWS,
+                "analyze_widths_totals: rows exceed the static scratch (262144 rows)");
+        require(samples >= 1 && samples <= EB_ANALYZE_MAX_SAMPLES,
+                "analyze_widths_totals: samples must be in [1, 32]");
+        EB_HIP(ebk::launch_analyze_widths_totals(static_cast<const uint16_t*>(w_f16), static_cast<int>(rows),
+                                                 static_cast<int>(cols), static_cast<const uint16_t*>(x_f16),
+                                                 static_cast<int>(samples), max_abs, totals,
+                                                 static_cast<hipStream_t>(stream)));
+    });
+}
+
 int eb_materialize_fp16(const eb_matrix* m, void* out_f16, void* stream) {
     return guarded([&] {                                 // runtime.cu:982-1022
         require(m && out_f16, "materialize: null pointer");

@@ -145,6 +145,14 @@ constexpr int kAnalyzeSums = 24;
 hipError_t launch_analyze_widths(const uint16_t* w, int N, int K, const uint16_t* x, int S, const float* max_abs,
                                  float* partials, hipStream_t stream);
 
+// The same width search with the per-tile partials in a static device array
+// (allocates nothing), reduced on the device into totals[kAnalyzeSums]
+// (double, device).  At most kAnalyzeScratchTiles tiles; calls that overlap
+// on one device share the array and race.
+constexpr int kAnalyzeScratchTiles = 16384;
+hipError_t launch_analyze_widths_totals(const uint16_t* w, int N, int K, const uint16_t* x, int S,
+                                        const float* max_abs, double* totals, hipStream_t stream);
+
 // Prefill tile shape: 0 auto, 1 128 x 256, 2 256 x 256 with four waves,
 // 3 256 x 256 with eight waves (process-wide).
 void set_prefill_tiles(int mode);

@@ -98,6 +98,7 @@ _sig("eb_benchmark", [_vp, _f32p, _i, ctypes.POINTER(_d)])
 _sig("eb_forward", [_vp, _vp, _i64, _vp, _vp, _vp])
 _sig("eb_forward_multi", [_vp, _i, _vp, _i64, _vp, _vp, _vp])
 _sig("eb_analyze_widths_device", [_vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp])
+_sig("eb_analyze_widths_device_totals", [_vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp])
 _sig("eb_materialize_fp16", [_vp, _vp, _vp])
 _sig("eb_unpack_codes", [_vp, _vp, _vp])
 _sig("eb_packed_linear", [_vp, _i, _i64, _vp, _vp, _i, _vp, _i, _i64, _i64, _i64, _vp, _vp])
@@ -247,6 +248,7 @@ def forward_torch_multi(matrices: Sequence["RuntimeMatrix"], input: torch.Tensor
 ANALYZE_TILE_ROWS = 16
 ANALYZE_MAX_SAMPLES = 32
 ANALYZE_SUMS = 24
+ANALYZE_STATIC_MAX_ROWS = 262144      # eb_analyze_widths_device_totals
 ANALYZE_WIDTHS = tuple(range(3, 16))
 
 
