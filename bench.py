@@ -150,6 +150,10 @@ def copies_of(layer, count: int):
 
 
 _SPIN_CYCLES_PER_MS = None
+# Untimed work right before every timed run.  After seconds of host-side
+# set-up the GPU starts below its working clock; with 2 ms of warm launches
+# the first shape timed after a compression still measured ~10% slow.
+WARM_MS = 25.0
 
 
 def _spin_cycles_per_ms() -> float:
@@ -177,7 +181,7 @@ def time_launches(launches, steps: int, warmup: int) -> float:
     on the launch stream.  Returns ms.
 
     A spin kernel first holds the stream long enough for the host to queue
-    everything after it: `warmup` untimed launches (and more, up to ~2 ms of
+    everything after it: `warmup` untimed launches (and more, up to WARM_MS of
     work, so the GPU runs at its working clock), the start event, the
     `steps` timed launches and the stop event.  The events then bracket
     exactly `steps` launches running back to back, and the host's enqueue
@@ -198,7 +202,7 @@ def time_launches(launches, steps: int, warmup: int) -> float:
             launches[i % len(launches)]()
         torch.cuda.synchronize()
         per_launch_ms = max((time.perf_counter() - t0) * 1e3 / min(steps, 50), 1e-4)
-    warm_n = max(warmup, min(5000, int(2.0 / per_launch_ms) + 1))
+    warm_n = max(warmup, min(20000, int(WARM_MS / per_launch_ms) + 1))
     hold_ms = 2.0
     for _ in range(6):
         start = torch.cuda.Event(enable_timing=True)
@@ -968,7 +972,7 @@ def main() -> int:
             "weight_copies_rotated": g["copies"],
             "bytes_per_step": g["bytes"],
             "timing": "HIP events on the launch stream around exactly `steps` launches, all queued behind a "
-                      "spin kernel and >= 2 ms of untimed warm launches",
+                      "spin kernel and >= 25 ms of untimed warm launches",
         },
         "roofline": {
             "bound": "hbm",

@@ -1658,16 +1658,18 @@ inline bool prefer_wide_tiles(int64_t M, int rows, int cus) {
 }
 
 // Whether 256 x 256 tiles run with eight waves (eb_prefill.hip) rather than
-// four.  Measured on MI355X (us, four -> eight waves): integer-code widths
-// up to 11 gain (14336 x 4096 M = 2048 b = 10 244.5 -> 238.1, b = 7
-// 242.1 -> 233.6; 11008 x 4096 M = 2048 b = 10 230.4 -> 207.7; 4096 x 4096
-// M = 8192 256.3 -> 246.6); b = 12 (258.1 -> 262.8), the decoded-fp16
-// widths (b = 13: 296.0 -> 334.3) and raw fp16 (241.5 -> 254.1) lose, and
-// keep four waves.
+// four.  Measured on MI355X, best of two interleaved runs after a 25 ms
+// warm-up (us, four -> eight waves): integer-code widths 8..11 gain
+// (14336 x 4096 M = 2048 b = 10 218.6 -> 215.2, b = 9 212.7 -> 211.0,
+// b = 8 209.5 -> 203.3; 4096 x 4096 M = 8192 b = 10 238.3 -> 236.6;
+// 14336 x 4096 M = 4096 b = 10 443.0 -> 427.4); b = 7 loses (214.3 ->
+// 219.0), and so do b = 12 (258.1 -> 262.8), the decoded-fp16 widths
+// (b = 13: 296.0 -> 334.3) and raw fp16 (241.5 -> 254.1), which keep four
+// waves; b <= 6 (not measured) keeps them too.
 template <int B, int MODE>
 inline bool prefill_eight_waves() {
     const int mode = g_prefill_tiles.load(std::memory_order_relaxed);
-    return mode == 3 || (mode == 0 && MODE == kModeQ && B <= 11);
+    return mode == 3 || (mode == 0 && MODE == kModeQ && B >= 8 && B <= 11);
 }
 
 // Tiles of linear_prefill_kernel with MI 32-row activation blocks: full

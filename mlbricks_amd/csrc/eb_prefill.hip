@@ -39,6 +39,14 @@
 // issued after the ones it needs.  Loads past the last step re-read the
 // last step (clamped addresses), which keeps every count uniform.
 //
+// Tried and slower: staging each 32-row block's weight bits once in LDS
+// (global_load_lds into a ring of three stages, then LDS reads before the
+// decode), which removes the duplicate loads of a column group and holds no
+// registers while in flight: 4-5% slower at b = 8..10 (configs[3] b = 10:
+// 225.5 against 215.2 us).  Without any weight-bit loads at all the kernel
+// took 189 against 244 us on another box, so what costs is the traffic and
+// latency of those bits, not the path they take.
+//
 // Launch: workgroup i runs on XCD i % 8, so each XCD walks a contiguous
 // range of tiles, four activation blocks at a time, and the workgroups it
 // runs at once share their activation and weight blocks in its L2.
