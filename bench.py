@@ -154,6 +154,8 @@ _SPIN_CYCLES_PER_MS = None
 # set-up the GPU starts below its working clock; with 2 ms of warm launches
 # the first shape timed after a compression still measured ~10% slow.
 WARM_MS = 25.0
+LEAD_LAUNCHES = 200
+CHUNK_LAUNCHES = 800
 
 
 def _spin_cycles_per_ms() -> float:
@@ -180,49 +182,59 @@ def time_launches(launches, steps: int, warmup: int) -> float:
     """Time exactly `steps` launches (cycling over `launches`) with HIP events
     on the launch stream.  Returns ms.
 
-    A spin kernel first holds the stream long enough for the host to queue
-    everything after it: `warmup` untimed launches (and more, up to WARM_MS of
-    work, so the GPU runs at its working clock), the start event, the
-    `steps` timed launches and the stop event.  The events then bracket
-    exactly `steps` launches running back to back, and the host's enqueue
-    cost stays outside whatever `steps` is.  (A captured graph replay was
-    measured to add ~4 us of device-side start-up per replay, which a short
-    run would charge to its few steps; eager launches behind the spin do
-    not.)"""
+    First WARM_MS (and at least `warmup`) of untimed launches run as fast as
+    the host issues them, so the GPU is at its working clock.  The timed
+    launches then go in chunks of at most CHUNK_LAUNCHES: for each, a spin
+    kernel holds the stream while the host queues behind it LEAD_LAUNCHES
+    untimed launches, the start event, the chunk and the stop event, so the
+    events bracket launches running back to back and the host's enqueue cost
+    stays outside them.  The result is the sum over the chunks.  A chunk
+    plus its lead stays within what the host can queue ahead of a held
+    stream: measured on MI355X, 1000 to 2000 of this library's decode
+    launches (their kernel arguments are ~400 bytes), beyond which the host
+    waits for the spin to end.  A captured graph replay was measured to add
+    ~4 us of device-side start-up per replay, which a short run would charge
+    to its few steps; eager launches behind the spin do not."""
     import torch
 
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
+    n = len(launches)
+    total = 0.0
     with torch.cuda.stream(stream):
-        for i in range(max(1, warmup)):
-            launches[i % len(launches)]()
+        launches[0]()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for i in range(min(steps, 50)):
-            launches[i % len(launches)]()
-        torch.cuda.synchronize()
-        per_launch_ms = max((time.perf_counter() - t0) * 1e3 / min(steps, 50), 1e-4)
-    warm_n = max(warmup, min(20000, int(WARM_MS / per_launch_ms) + 1))
-    hold_ms = 2.0
-    for _ in range(6):
-        start = torch.cuda.Event(enable_timing=True)
-        stop = torch.cuda.Event(enable_timing=True)
-        with torch.cuda.stream(stream):
-            t_host = time.perf_counter()
-            torch.cuda._sleep(int(_spin_cycles_per_ms() * hold_ms))
-            for i in range(warm_n):
-                launches[(i - warm_n) % len(launches)]()
-            start.record(stream)
-            for i in range(steps):
-                launches[i % len(launches)]()
-            stop.record(stream)
-            enqueue_ms = (time.perf_counter() - t_host) * 1e3
-        stop.synchronize()
-        torch.cuda.synchronize()
-        if enqueue_ms < 0.8 * hold_ms:
-            return float(start.elapsed_time(stop))
-        hold_ms = 2.0 * enqueue_ms          # the host was slower than the spin: hold longer
-    raise RuntimeError("could not queue the timed launches ahead of the GPU")
+        done = 0
+        while (time.perf_counter() - t0) * 1e3 < WARM_MS or done < warmup:
+            launches[done % n]()
+            done += 1
+        per_launch_ms = (time.perf_counter() - t0) * 1e3 / done
+        first = 0
+        while first < steps:
+            count = min(CHUNK_LAUNCHES, steps - first)
+            hold_ms = 1.5 * (LEAD_LAUNCHES + count) * per_launch_ms + 1.0
+            for _ in range(6):
+                start = torch.cuda.Event(enable_timing=True)
+                stop = torch.cuda.Event(enable_timing=True)
+                t_host = time.perf_counter()
+                torch.cuda._sleep(int(_spin_cycles_per_ms() * hold_ms))
+                for i in range(first - LEAD_LAUNCHES, first):
+                    launches[i % n]()
+                start.record(stream)
+                for i in range(first, first + count):
+                    launches[i % n]()
+                stop.record(stream)
+                enqueue_ms = (time.perf_counter() - t_host) * 1e3
+                stop.synchronize()
+                if enqueue_ms < 0.8 * hold_ms:
+                    break
+                hold_ms = 2.0 * enqueue_ms  # the host was slower than the spin: hold longer
+            else:
+                raise RuntimeError("could not queue the timed launches ahead of the GPU")
+            total += float(start.elapsed_time(stop))
+            first += count
+    return total
 
 
 def bench_gemv(args) -> dict:
@@ -753,10 +765,14 @@ def counter_probe(args) -> int:
 
 
 def summarize_counters(paths: list[str]) -> int:
-    """Per-kernel averages of counter passes over `--counter-probe` (first
-    dispatch of each kernel dropped as warm-up), with the clock (GRBM_GUI_ACTIVE
-    per XCD over the dispatch's duration) and the MFMA-busy fraction of the
-    SIMDs over those cycles."""
+    """Per-kernel averages of counter passes over `--counter-probe`, with the
+    clock (GRBM_GUI_ACTIVE per XCD over the dispatch's duration) and the
+    MFMA-busy fraction of the SIMDs over those cycles.  Of each kernel only
+    the launch shape (name, grid) that ran most often counts, without its
+    first dispatch (warm-up): the calibration forwards of the compression
+    run hipBLASLt GEMMs of other shapes.  Clock and MFMA-busy are left out
+    for kernels under 20 us, where the counter's window around the dispatch
+    is not small beside it."""
     import collections
     import csv
     import statistics
@@ -768,20 +784,19 @@ def summarize_counters(paths: list[str]) -> int:
         for r in csv.DictReader(open(path, newline="")):
             d = per[int(r["Dispatch_Id"])]
             d["name"] = r["Kernel_Name"]
+            d["shape"] = (r["Kernel_Name"], r["Grid_Size"])
             d[r["Counter_Name"]] = float(r["Counter_Value"])
             d["duration_us"] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
-        seen = collections.Counter()
+        runs: dict[str, dict[tuple, list[dict]]] = collections.defaultdict(lambda: collections.defaultdict(list))
         for did in sorted(per):
-            d = per[did]
-            key = next((w for w in wanted if w in d["name"]), None)
-            if key is None:
-                continue
-            seen[key] += 1
-            if seen[key] == 1:
-                continue                      # warm-up dispatch
-            for k, v in d.items():
-                if k != "name":
-                    table[key][k].append(v)
+            key = next((w for w in wanted if w in per[did]["name"]), None)
+            if key is not None:
+                runs[key][per[did]["shape"]].append(per[did])
+        for key, shapes in runs.items():
+            for d in max(shapes.values(), key=len)[1:]:      # first dispatch: warm-up
+                for k, v in d.items():
+                    if k not in ("name", "shape"):
+                        table[key][k].append(v)
     cols = sorted({k for t in table.values() for k in t if k not in ("duration_us",)})
     lines = ["| kernel | dispatches | us | clock GHz | MFMA busy | " + " | ".join(cols) + " |",
              "|---" * (len(cols) + 5) + "|"]
@@ -791,7 +806,7 @@ def summarize_counters(paths: list[str]) -> int:
         t = table[key]
         avg = {k: statistics.mean(v) for k, v in t.items()}
         n = max(len(v) for v in t.values())
-        grbm = avg.get("GRBM_GUI_ACTIVE", 0.0) / 8                  # eight XCDs
+        grbm = avg.get("GRBM_GUI_ACTIVE", 0.0) / 8 if avg["duration_us"] >= 20 else 0.0   # eight XCDs
         ghz = grbm / (avg["duration_us"] * 1e3) if grbm else float("nan")
         busy = avg["SQ_VALU_MFMA_BUSY_CYCLES"] / (grbm * 1024) if grbm and "SQ_VALU_MFMA_BUSY_CYCLES" in avg \
             else float("nan")
@@ -971,8 +986,9 @@ def main() -> int:
             "storage_bits": g["bits"],
             "weight_copies_rotated": g["copies"],
             "bytes_per_step": g["bytes"],
-            "timing": "HIP events on the launch stream around exactly `steps` launches, all queued behind a "
-                      "spin kernel and >= 25 ms of untimed warm launches",
+            "timing": "HIP events on the launch stream around exactly `steps` launches, after >= 25 ms of "
+                      "untimed warm launches, in chunks of <= 800 launches each queued behind its own spin "
+                      "kernel and 200 untimed launches; the sum over the chunks",
         },
         "roofline": {
             "bound": "hbm",
