@@ -178,9 +178,10 @@ def _spin_cycles_per_ms() -> float:
     return _SPIN_CYCLES_PER_MS
 
 
-def time_launches(launches, steps: int, warmup: int) -> float:
+def time_launches(launches, steps: int, warmup: int, kernels_per_launch: int = 1) -> float:
     """Time exactly `steps` launches (cycling over `launches`) with HIP events
-    on the launch stream.  Returns ms.
+    on the launch stream.  Returns ms.  A launch may issue several kernels
+    (`kernels_per_launch`); the limits below count kernels.
 
     First WARM_MS (and at least `warmup`) of untimed launches run as fast as
     the host issues them, so the GPU is at its working clock.  The timed
@@ -210,16 +211,18 @@ def time_launches(launches, steps: int, warmup: int) -> float:
             launches[done % n]()
             done += 1
         per_launch_ms = (time.perf_counter() - t0) * 1e3 / done
+        lead = max(1, LEAD_LAUNCHES // kernels_per_launch)
+        chunk = max(1, CHUNK_LAUNCHES // kernels_per_launch)
         first = 0
         while first < steps:
-            count = min(CHUNK_LAUNCHES, steps - first)
-            hold_ms = 1.5 * (LEAD_LAUNCHES + count) * per_launch_ms + 1.0
+            count = min(chunk, steps - first)
+            hold_ms = 1.5 * (lead + count) * per_launch_ms + 1.0
             for _ in range(6):
                 start = torch.cuda.Event(enable_timing=True)
                 stop = torch.cuda.Event(enable_timing=True)
                 t_host = time.perf_counter()
                 torch.cuda._sleep(int(_spin_cycles_per_ms() * hold_ms))
-                for i in range(first - LEAD_LAUNCHES, first):
+                for i in range(first - lead, first):
                     launches[i % n]()
                 start.record(stream)
                 for i in range(first, first + count):
@@ -591,10 +594,10 @@ def bolt_decode(args) -> int:
 
     tokens = 20
     rows = []
-    for label, fn in (("96 Linears + LM head", token_separate),
-                      ("q/k/v/head_gate fused + LM head", token_fused),
-                      ("LM head alone", head_only)):
-        us = time_launches([fn], tokens, 3) / tokens * 1e3
+    for label, fn, kernels in (("96 Linears + LM head", token_separate, 97),
+                               ("q/k/v/head_gate fused + LM head", token_fused, 97),
+                               ("LM head alone", head_only, 1)):
+        us = time_launches([fn], tokens, 3, kernels) / tokens * 1e3
         rows.append((label, us))
         log(f"  {label}: {us:.1f} us per token")
     head_us = rows[2][1]

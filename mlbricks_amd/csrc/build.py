@@ -24,7 +24,7 @@ LIB_NAME = "libelasticbit_hip.so"
 
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 ARCH = "gfx950"
-DEVICE_SOURCES = ("eb_kernels.hip", "eb_prefill.hip", "eb_analyze.hip")
+DEVICE_SOURCES = ("eb_kernels.hip", "eb_prefill.hip", "eb_decode_rows.hip", "eb_analyze.hip")
 HOST_SOURCES = ("eb_host.cpp",)
 
 # Packed-fp32 VALU forms are disabled for every device compile on this target.

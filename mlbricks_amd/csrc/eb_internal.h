@@ -164,6 +164,16 @@ void set_prefill_tiles(int mode);
 hipError_t launch_prefill_pp(const DevMatrix& m, int mode, const uint16_t* x, int64_t M, uint16_t* y,
                              const uint16_t* bias, hipStream_t stream);
 
+// Batched decode with several row tiles per workgroup (eb_decode_rows.hip).
+// decode_rows_per_workgroup: the row tiles per workgroup it takes for this
+// call (2..4), or 0 where linear_decode_kernel is used: 8 <= M <= 16, b <=
+// kDecodeRowsMaxBits (not raw fp16), cols <= 4096, and more row tiles than
+// CUs (two per CU from M = 12).  mode as for launch_prefill_pp.
+constexpr int kDecodeRowsMaxBits = 12;
+int decode_rows_per_workgroup(int64_t M, const DevMatrix& m, int mode, int cus);
+hipError_t launch_decode_rows(const DevMatrix& m, int mode, int rt, const uint16_t* x, int64_t M, uint16_t* y,
+                              const uint16_t* bias, int xvec, hipStream_t stream);
+
 // Legacy flat-group op (bolt/ops_cuda.cu:2708-2795).
 hipError_t launch_packed_linear(const void* x, int x_dtype, int64_t M, const uint8_t* packed,
                                 const void* scales, int scale_dtype, const void* bias, int bits,

@@ -359,6 +359,7 @@ __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
     constexpr int CT = MB == 1 ? 16 : 8;
     constexpr int kBpc = CT / kBatch;
     static_assert(XL != 3 || (kBpc >= 1 && CT % kBatch == 0), "a chunk holds whole workgroup batches");
+    static_assert(XL != 3 || WAVES == 8, "stage_chunk issues Mp * CT / 32 loads per wave: eight waves per chunk");
     extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   // XL = 1, 2: [M][spr * 128]; XL = 3: two chunks
 
     const int tile = select_matrix(mt, m, y, bias);
@@ -1789,6 +1790,8 @@ hipError_t run_linear_mode(const DevMatrix& m, const uint16_t* x, int64_t M, uin
     if (M == 1 && xvec == 2 && gemv_takes<B, MODE>(m)) {
         hipLaunchKernelGGL((linear_gemv_kernel<B, MODE>), dim3(tiles), dim3(64 * kGemvWaves),
                            static_cast<size_t>(m.cols) * 2, s, m, x, y, bias, mt);
+    } else if (const int rt = mt.count == 1 ? decode_rows_per_workgroup(M, m, MODE, device_cu_count()) : 0; rt > 0) {
+        return launch_decode_rows(m, MODE, rt, x, M, y, bias, xvec, s);
     } else if (M <= 16 || (M <= kDecodeMaxM && (mt.count > 1 || prefer_decode(M, m, device_cu_count())))) {
         if (M <= 16) {
             launch_decode<B, MODE, 1>(m, x, M, y, bias, xvec, s, mt, tiles);
@@ -1897,8 +1900,15 @@ hipError_t launch_linear_multi(const DevMatrix* ms, int count, bool exact_w16, c
     for (int j = 1; j < count; ++j) {
         if (ms[j].cols != ms[0].cols || ms[j].bits != ms[0].bits) return hipErrorInvalidValue;
     }
+    // A matrix that its own forward sends to linear_decode_rows_kernel fills
+    // the device by itself; the group then runs per matrix, so that every
+    // output equals that forward's bit for bit.
     bool fused = M <= kDecodeMaxM;
-    for (int j = 0; j < count && fused; ++j) fused = prefer_decode(M, ms[j], device_cu_count());
+    const int cus = device_cu_count();
+    for (int j = 0; j < count && fused; ++j) {
+        const int mode = ms[j].bits == 16 ? kModeRaw : (ms[j].bits <= 12 && !exact_w16 ? kModeQ : kModeW);
+        fused = prefer_decode(M, ms[j], cus) && decode_rows_per_workgroup(M, ms[j], mode, cus) == 0;
+    }
     if (!fused) {
         for (int j = 0; j < count; ++j) {
             const hipError_t e = run_linear(ms[j], exact_w16, x, M, ys[j], biases ? biases[j] : nullptr, stream,

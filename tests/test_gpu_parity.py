@@ -736,9 +736,11 @@ def test_decode_with_more_row_tiles_than_cus(native, rows, M):
 
 @pytest.mark.parametrize("M", [16, 17])
 def test_multi_matrix_decode_over_large_matrices(native, M):
-    """A multi-matrix decode launch over 1632 row tiles (Gate/Up: two
-    11008 x 4096 matrices and a 4096 x 4096 one) with x staged whole returns
-    each matrix's own forward bit for bit."""
+    """A multi-matrix decode over 1632 row tiles (Gate/Up: two 11008 x 4096
+    matrices and a 4096 x 4096 one) returns each matrix's own forward bit for
+    bit: at M = 17 as one launch with x staged whole; at M = 16, where the
+    11008-row matrices' own forwards take the row-blocked kernel, as one
+    launch per matrix."""
     cols = 4096
     rng = np.random.default_rng(900 + M)
     mats = []
