@@ -618,14 +618,14 @@ def m_sweep(args) -> int:
     copy other than the last ones read (>= 512 MB of rotated copies, twice
     the MALL), so no M is helped by a warm cache.  Shows where the launcher
     moves between its kernels (GEMV, decode with 1/2/4 activation blocks,
-    prefill tiles)."""
+    row-blocked decode, prefill tiles)."""
     import numpy as np
     import torch
 
     from mlbricks_amd.elasticbit import _native as native
 
     shapes = ((4096, 4096), (11008, 4096), (4096, 11008), (14336, 4096), (1024, 1024), (1536, 384))
-    Ms = (1, 4, 16, 17, 32, 64, 96, 128, 256, 512, 1024, 2048)
+    Ms = (1, 4, 8, 12, 16, 17, 32, 64, 96, 128, 256, 512, 1024, 2048)
     lines = ["| N x K | " + " | ".join(f"M={M}" for M in Ms) + " |", "|---" * (len(Ms) + 1) + "|"]
     for rows, cols in shapes:
         rng = np.random.default_rng(rows + cols)
