@@ -364,7 +364,36 @@ def ceiling_curve(args) -> int:
         lines.append(f"| {nbytes:,} | {r['us_per_launch']:.3f} | {r['gbs']:.0f} | {100 * r['frac_hbm_peak']:.1f} | "
                      f"{r['launch']} |")
     print("\n".join(lines), flush=True)
+    print("\n" + vendor_reads(args), flush=True)
     return 0
+
+
+def vendor_reads(args) -> str:
+    """Kernels this build did not write, reading about the same bytes per
+    launch, timed the same way over rotated copies: torch's sum over an fp16
+    tensor (a reduction) and torch.matmul of one fp16 row by an fp16 matrix
+    (hipBLASLt's M = 1 GEMM).  Independent points beside the probe for what
+    one launch of that size reaches."""
+    import torch
+
+    lines = ["| kernel | bytes per launch | us per launch | GB/s | % of 8 TB/s |", "|---|---|---|---|---|"]
+    for rows, cols in ((4096, 2560), (11008, 2560), (16384, 16384)):
+        nbytes = 2 * rows * cols
+        copies = max(2, -(-2 * MALL_BYTES // nbytes) + 1)
+        steps = max(20, min(args.steps, int(2e6 // max(nbytes >> 10, 1))))
+        ws = [torch.randn(rows, cols, device="cuda").half() for _ in range(copies)]
+        x = torch.randn(1, cols, device="cuda").half()
+        ys = [torch.empty(1, rows, dtype=torch.float16, device="cuda") for _ in ws]
+        outs = [torch.empty((), dtype=torch.float16, device="cuda") for _ in ws]
+        for label, fns in (("torch.sum (fp16)", [lambda w=w, o=o: torch.sum(w, dim=(0, 1), out=o) for w, o in zip(ws, outs)]),
+                           ("torch.matmul, M = 1 (hipBLASLt)",
+                            [lambda w=w, y=y: torch.matmul(x, w.t(), out=y) for w, y in zip(ws, ys)])):
+            us = time_launches(fns, steps, max(3, steps // 10)) / steps * 1e3
+            lines.append(f"| {label} | {nbytes:,} | {us:.3f} | {nbytes / us / 1e3:.0f} | "
+                         f"{nbytes / us / 1e3 / HBM_PEAK_GBS * 100:.1f} |")
+            log(f"vendor read: {label} {nbytes / 1e6:.1f} MB: {us:.3f} us")
+        del ws, ys, outs
+    return "\n".join(lines)
 
 
 def reference_route(args) -> dict:
