@@ -561,6 +561,15 @@ __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
 // Only activation row 0 of the A operand is non-zero, so D[0][n] (lane n,
 // element 0) holds row n's partial sum; the 16 partials of a row are added
 // in wave order, so results are deterministic.
+//
+// Each wave stages only the activations of its own two tiles (256 columns,
+// 512 B of LDS per wave, one 32-lane global_load_lds) and waits on its own
+// loads, so no workgroup barrier stands between the loads and the MFMAs.
+// Per-wave clock stamps of the earlier form, where the workgroup staged all
+// of x and passed a barrier first, showed the waves spending ~1.2 us of a
+// ~3.7 us life until that barrier; measured on MI355X (us, that form ->
+// this): 4096^2 b = 10 5.668 -> 5.643, b = 9 5.404 -> 5.358, 11008 x 4096
+// 11.6 -> 11.33, 14336 x 4096 14.43 -> 13.99, 4096 x 3072 5.26 -> 5.11.
 // ---------------------------------------------------------------------------
 
 constexpr int kGemvWaves = 16;
@@ -571,7 +580,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void linear_gemv_kernel(
     DevMatrix m, const uint16_t* __restrict__ x, uint16_t* __restrict__ y, const uint16_t* __restrict__ bias,
     const MultiTail mt) {
     using Bits = GroupBits<B, MODE>;
-    extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   // [cols], cols % 128 == 0
+    extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   // [kGemvWaves][2][128]
     __shared__ float red[kGemvWaves][kTileRows];
 
     const int tile = select_matrix(mt, m, y, bias);
@@ -589,27 +598,31 @@ __global__ __launch_bounds__(64 * kGemvWaves) void linear_gemv_kernel(
         if constexpr (MODE == kModeQ) out_scale = m.scales[row];
         if (bias) out_bias = bias[row];
     }
-    // x goes global -> LDS, one 16-byte vector per thread (cols / 8 <= 512)
-    const int nv = m.cols / 8;
-    if (static_cast<int>(threadIdx.x) < nv) {
-        __builtin_amdgcn_global_load_lds(x + 8 * threadIdx.x, (lds_void_ptr)(xs + 8 * (threadIdx.x & ~63u)), 16, 0,
-                                         0);
+    // The x of this wave's steps (lanes 0-15: step wave, lanes 16-31: step
+    // wave + 16, sixteen 16-byte vectors each; cols == spr * 128) goes
+    // global -> LDS into this wave's 512 bytes.  A step past the last is
+    // staged as the last one and multiplied by zero.
+    uint16_t* xw = xs + wave * (2 * kTileGroups * kGroup);
+    {
+        const int st = min(wave + kGemvWaves * (lane >> 4), steps - 1);
+        if (lane < 32)
+            __builtin_amdgcn_global_load_lds(x + 8 * (st * 16 + (lane & 15)), (lds_void_ptr)xw, 16, 0, 0);
     }
     const size_t slot0 = static_cast<size_t>(tile) * steps * kTileSlots + lane;
     Bits b0, b1;
     b0.load(m, slot0 + static_cast<size_t>(min(wave, steps - 1)) * kTileSlots);
     b1.load(m, slot0 + static_cast<size_t>(min(wave + kGemvWaves, steps - 1)) * kTileSlots);
-    // everything but the two weight tiles (scales, bias, x) has landed
+    // everything but the two weight tiles (scales, bias, this wave's x) has
+    // landed; no other wave's x is read
     wait_vmcnt<2 * GroupLoads<B, MODE>::value>();
-    barrier_after_wait();
 
     floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     auto mul = [&](const Bits& bits, int st) {
         const bool ok = st < steps;
-        const int k0 = (min(st, steps - 1) * kTileGroups + quarter) * kGroup;
+        const int k0 = (st >= kGemvWaves ? kTileGroups * kGroup : 0) + quarter * kGroup;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            const half8 xa = *reinterpret_cast<const half8*>(xs + k0 + 8 * t);   // broadcast per quarter
+            const half8 xa = *reinterpret_cast<const half8*>(xw + k0 + 8 * t);   // broadcast per quarter
             const half8 a = (ok && nl == 0) ? xa : half8{0, 0, 0, 0, 0, 0, 0, 0};
             half8 b = bits.operand(t, s);
             if constexpr (MODE == kModeRaw) {
@@ -1625,17 +1638,19 @@ constexpr int kDecodeMaxM = 64;
 // b = 15).  Measured on MI355X at M = 1 over rotated copies:
 // with K at most 16 tiles (2048 columns) half or more of the 16 waves idle
 // and the decode kernel is faster (4096 x 1024: 3.4-3.9 us against
-// 3.7-5.3 us; 4096 x 2048 from b = 10); at b = 11 the two are even or the
-// decode kernel ahead (4096 x 3072: 5.59 against 6.24 us); at b <= 7 with
-// more than 256 row tiles (at most 28 bytes per lane and group) the decode
-// kernel is 4-11% faster (14336 x 4096 b = 4: 8.0 against 9.0 us, b = 7:
-// 11.7 against 12.5 us).  Elsewhere the GEMV kernel is ahead by up to 24%
-// (1024 x 4096).
+// 3.7-5.3 us; 4096 x 2048 from b = 10); at b = 11 (the largest group
+// loads) the GEMV kernel leads only with every wave holding two tiles,
+// K = 4096 (4096 x 4096: 6.26 against 6.57 us; 11008 x 4096: 13.47
+// against 13.60), and trails at 4096 x 3072 (5.84 against 5.74); at b <= 7
+// with more than 256 row tiles (at most 28 bytes per lane and group) the
+// decode kernel is 4-6% faster (14336 x 4096 b = 4: 8.3 against 8.7 us,
+// b = 7: 12.3 against 13.0).  Elsewhere the GEMV kernel is ahead by up to
+// 24% (1024 x 4096).
 template <int B, int MODE>
 inline bool gemv_takes(const DevMatrix& m) {
     if (MODE == kModeW) return false;
     if (m.spr <= kGemvMaxSteps / 2 || m.spr > kGemvMaxSteps) return false;
-    if (MODE != kModeRaw && (B == 11 || (B <= 7 && m.rtiles > 256))) return false;
+    if (MODE != kModeRaw && ((B == 11 && m.spr != kGemvMaxSteps) || (B <= 7 && m.rtiles > 256))) return false;
     return true;
 }
 
@@ -1789,7 +1804,7 @@ hipError_t run_linear_mode(const DevMatrix& m, const uint16_t* x, int64_t M, uin
                            (MODE == kModeRaw || groups * 32u < (uint64_t(1) << 32));
     if (M == 1 && xvec == 2 && gemv_takes<B, MODE>(m)) {
         hipLaunchKernelGGL((linear_gemv_kernel<B, MODE>), dim3(tiles), dim3(64 * kGemvWaves),
-                           static_cast<size_t>(m.cols) * 2, s, m, x, y, bias, mt);
+                           static_cast<size_t>(kGemvWaves) * 2 * kTileGroups * kGroup * 2, s, m, x, y, bias, mt);
     } else if (const int rt = mt.count == 1 ? decode_rows_per_workgroup(M, m, MODE, device_cu_count()) : 0; rt > 0) {
         return launch_decode_rows(m, MODE, rt, x, M, y, bias, xvec, s);
     } else if (M <= 16 || (M <= kDecodeMaxM && (mt.count > 1 || prefer_decode(M, m, device_cu_count())))) {
