@@ -548,7 +548,7 @@ __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// GEMV, M = 1, K at most 32 tiles (4096 columns): one workgroup of 16 waves
+// GEMV, M <= 4, K at most 32 tiles (4096 columns): one workgroup of 16 waves
 // owns one row tile and wave w takes its tiles w and w + 16, so every
 // weight tile of the workgroup is requested at once, before the wave waits
 // for anything.  On MI355X a 4096 x 4096 b = 10 matrix spreads as 16 waves
@@ -558,13 +558,14 @@ __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
 // flight per CU than the memory system serves well), so those keep
 // linear_decode_kernel.
 //
-// Only activation row 0 of the A operand is non-zero, so D[0][n] (lane n,
-// element 0) holds row n's partial sum; the 16 partials of a row are added
-// in wave order, so results are deterministic.
+// Only activation rows 0 .. M-1 of the A operand are non-zero, so D[e][n]
+// (lane n, element e) holds row n's partial sum for activation row e; the
+// 16 partials are added in wave order, so results are deterministic.
 //
-// Each wave stages only the activations of its own two tiles (256 columns,
-// 512 B of LDS per wave, one 32-lane global_load_lds) and waits on its own
-// loads, so no workgroup barrier stands between the loads and the MFMAs.
+// Each wave stages only the activations of its own two tiles (256 columns
+// of M rows, 512 B of LDS per row, one 32-lane global_load_lds per row) and
+// waits on its own loads, so no workgroup barrier stands between the loads
+// and the MFMAs.
 // Per-wave clock stamps of the earlier form, where the workgroup staged all
 // of x and passed a barrier first, showed the waves spending ~1.2 us of a
 // ~3.7 us life until that barrier; measured on MI355X (us, that form ->
@@ -574,14 +575,18 @@ __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
 
 constexpr int kGemvWaves = 16;
 constexpr int kGemvMaxSteps = 2 * kGemvWaves;
+constexpr int kGemvMaxM = 4;                 // activation rows: lanes 0-15 hold D rows 0-3
 
-template <int B, int MODE>
+// MR: 1 (M = 1, every row count a compile-time 1) or kGemvMaxM (M = 2..4).
+template <int B, int MODE, int MR>
 __global__ __launch_bounds__(64 * kGemvWaves) void linear_gemv_kernel(
-    DevMatrix m, const uint16_t* __restrict__ x, uint16_t* __restrict__ y, const uint16_t* __restrict__ bias,
-    const MultiTail mt) {
+    DevMatrix m, const uint16_t* __restrict__ x, int m_rows, uint16_t* __restrict__ y,
+    const uint16_t* __restrict__ bias, const MultiTail mt) {
     using Bits = GroupBits<B, MODE>;
-    extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   // [kGemvWaves][2][128]
-    __shared__ float red[kGemvWaves][kTileRows];
+    constexpr int kXRow = 2 * kTileGroups * kGroup;                  // halves of one row's two steps
+    extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   // [kGemvWaves][M][2][128]
+    __shared__ float red[kGemvWaves][MR][kTileRows];
+    const int M = MR == 1 ? 1 : m_rows;
 
     const int tile = select_matrix(mt, m, y, bias);
     const int lane = threadIdx.x & 63;
@@ -592,21 +597,26 @@ __global__ __launch_bounds__(64 * kGemvWaves) void linear_gemv_kernel(
     const int row = tile * kTileRows + nl;
     float s = 0.0f;
     if constexpr (MODE == kModeW) s = row < m.rows ? m.scales[row] : 0.0f;
+    // thread o < 16 M stores output (o / 16, row of n = o % 16) at the end
+    const int on = tile * kTileRows + (threadIdx.x & 15);
     float out_scale = 1.0f;
     uint16_t out_bias = 0;
-    if (threadIdx.x < kTileRows && row < m.rows) {
-        if constexpr (MODE == kModeQ) out_scale = m.scales[row];
-        if (bias) out_bias = bias[row];
+    if (static_cast<int>(threadIdx.x) < kTileRows * M && on < m.rows) {
+        if constexpr (MODE == kModeQ) out_scale = m.scales[on];
+        if (bias) out_bias = bias[on];
     }
-    // The x of this wave's steps (lanes 0-15: step wave, lanes 16-31: step
-    // wave + 16, sixteen 16-byte vectors each; cols == spr * 128) goes
-    // global -> LDS into this wave's 512 bytes.  A step past the last is
-    // staged as the last one and multiplied by zero.
-    uint16_t* xw = xs + wave * (2 * kTileGroups * kGroup);
-    {
-        const int st = min(wave + kGemvWaves * (lane >> 4), steps - 1);
-        if (lane < 32)
-            __builtin_amdgcn_global_load_lds(x + 8 * (st * 16 + (lane & 15)), (lds_void_ptr)xw, 16, 0, 0);
+    // The x of this wave's steps goes global -> LDS into this wave's M x 512
+    // bytes: vector v (row v / 32, step wave + 16 ((v / 16) % 2), 16-byte
+    // vector v % 16 of that step; cols == spr * 128).  A step past the last
+    // is staged as the last one and multiplied by zero.
+    uint16_t* xw = xs + wave * M * kXRow;
+    for (int k = 0; 32 * M > 64 * k; ++k) {
+        const int v = 64 * k + lane;
+        if (v < 32 * M) {
+            const int st = min(wave + kGemvWaves * ((v >> 4) & 1), steps - 1);
+            __builtin_amdgcn_global_load_lds(x + static_cast<size_t>(v >> 5) * m.cols + 8 * (st * 16 + (v & 15)),
+                                             (lds_void_ptr)(xw + 512 * k), 16, 0, 0);
+        }
     }
     const size_t slot0 = static_cast<size_t>(tile) * steps * kTileSlots + lane;
     Bits b0, b1;
@@ -617,13 +627,15 @@ __global__ __launch_bounds__(64 * kGemvWaves) void linear_gemv_kernel(
     wait_vmcnt<2 * GroupLoads<B, MODE>::value>();
 
     floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    const bool xok = nl < M;
+    const uint16_t* xr = xw + (xok ? nl : 0) * kXRow;
     auto mul = [&](const Bits& bits, int st) {
         const bool ok = st < steps;
         const int k0 = (st >= kGemvWaves ? kTileGroups * kGroup : 0) + quarter * kGroup;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            const half8 xa = *reinterpret_cast<const half8*>(xw + k0 + 8 * t);   // broadcast per quarter
-            const half8 a = (ok && nl == 0) ? xa : half8{0, 0, 0, 0, 0, 0, 0, 0};
+            const half8 xa = *reinterpret_cast<const half8*>(xr + k0 + 8 * t);   // broadcast per quarter and row
+            const half8 a = (ok && xok) ? xa : half8{0, 0, 0, 0, 0, 0, 0, 0};
             half8 b = bits.operand(t, s);
             if constexpr (MODE == kModeRaw) {
                 // past the last tile the reloaded raw weights may hold Inf or NaN
@@ -635,13 +647,20 @@ __global__ __launch_bounds__(64 * kGemvWaves) void linear_gemv_kernel(
     mul(b0, wave);
     mul(b1, wave + kGemvWaves);
 
-    if (lane < kTileRows) red[wave][lane] = acc[0];
+    // D[e][n] of activation row e < M sits in lane n < 16, element e
+    if (lane < kTileRows) {
+#pragma unroll
+        for (int e = 0; e < MR; ++e) {
+            if (e < M) red[wave][e][lane] = acc[e];
+        }
+    }
     __syncthreads();
-    if (threadIdx.x < kTileRows && row < m.rows) {
+    if (static_cast<int>(threadIdx.x) < kTileRows * M && on < m.rows) {
+        const int e = threadIdx.x >> 4;
         float v = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kGemvWaves; ++w) v += red[w][threadIdx.x];
-        y[row] = epilogue<MODE>(v, out_scale, bias != nullptr, out_bias);
+        for (int w = 0; w < kGemvWaves; ++w) v += red[w][e][threadIdx.x & 15];
+        y[static_cast<size_t>(e) * m.rows + on] = epilogue<MODE>(v, out_scale, bias != nullptr, out_bias);
     }
 }
 
@@ -1654,6 +1673,18 @@ inline bool gemv_takes(const DevMatrix& m) {
     return true;
 }
 
+// Whether linear_gemv_kernel takes 2 <= M <= 4: the integer-code arithmetic
+// where it takes M = 1, except b = 11.  Measured on MI355X (us, decode
+// kernel -> GEMV kernel, b = 10, M = 2 / 4): 4096 x 4096 6.28 -> 5.79 /
+// 6.45 -> 5.96; 11008 x 4096 11.98 -> 11.64 / 12.57 -> 11.99; 14336 x 4096
+// 15.09 -> 14.41 / 15.54 -> 15.15; 4096 x 3072 5.42 -> 5.27 / 5.60 -> 5.44;
+// b = 9 at 11008 x 4096 M = 4 11.51 -> 11.19.  At b = 11 the two are even
+// (+-1%); raw fp16 (b = 16) is 1-2% slower there.
+template <int B, int MODE>
+inline bool gemv_rows_takes(const DevMatrix& m) {
+    return MODE == kModeQ && B != 11 && gemv_takes<B, MODE>(m);
+}
+
 // Whether the 256 x 256 prefill tiles finish before the 128 x 256 ones.
 // Cost in rounds of 128 x 256 tiles over the CUs: a 256 x 256 tile takes
 // about 1.7 of them (measured on MI355X, 14336 x 4096 b = 10: 116 us per
@@ -1803,8 +1834,12 @@ hipError_t run_linear_mode(const DevMatrix& m, const uint16_t* x, int64_t M, uin
     const bool offsets32 = static_cast<uint64_t>(M) * m.cols * 2 < (uint64_t(1) << 32) &&
                            (MODE == kModeRaw || groups * 32u < (uint64_t(1) << 32));
     if (M == 1 && xvec == 2 && gemv_takes<B, MODE>(m)) {
-        hipLaunchKernelGGL((linear_gemv_kernel<B, MODE>), dim3(tiles), dim3(64 * kGemvWaves),
-                           static_cast<size_t>(kGemvWaves) * 2 * kTileGroups * kGroup * 2, s, m, x, y, bias, mt);
+        hipLaunchKernelGGL((linear_gemv_kernel<B, MODE, 1>), dim3(tiles), dim3(64 * kGemvWaves),
+                           static_cast<size_t>(kGemvWaves) * 2 * kTileGroups * kGroup * 2, s, m, x, 1, y, bias, mt);
+    } else if (M <= kGemvMaxM && xvec == 2 && gemv_rows_takes<B, MODE>(m)) {
+        hipLaunchKernelGGL((linear_gemv_kernel<B, MODE, kGemvMaxM>), dim3(tiles), dim3(64 * kGemvWaves),
+                           static_cast<size_t>(kGemvWaves) * M * 2 * kTileGroups * kGroup * 2, s, m, x,
+                           static_cast<int>(M), y, bias, mt);
     } else if (const int rt = mt.count == 1 ? decode_rows_per_workgroup(M, m, MODE, device_cu_count()) : 0; rt > 0) {
         return launch_decode_rows(m, MODE, rt, x, M, y, bias, xvec, s);
     } else if (M <= 16 || (M <= kDecodeMaxM && (mt.count > 1 || prefer_decode(M, m, device_cu_count())))) {
