@@ -548,7 +548,7 @@ __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// GEMV, M <= 4, K at most 32 tiles (4096 columns): one workgroup of 16 waves
+// GEMV, M <= 16, K at most 32 tiles (4096 columns): one workgroup of 16 waves
 // owns one row tile and wave w takes its tiles w and w + 16, so every
 // weight tile of the workgroup is requested at once, before the wave waits
 // for anything.  On MI355X a 4096 x 4096 b = 10 matrix spreads as 16 waves
@@ -575,9 +575,10 @@ __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
 
 constexpr int kGemvWaves = 16;
 constexpr int kGemvMaxSteps = 2 * kGemvWaves;
-constexpr int kGemvMaxM = 4;                 // activation rows: lanes 0-15 hold D rows 0-3
+constexpr int kGemvMaxM = 4;                 // M up to this: lanes 0-15 hold all of D
 
-// MR: 1 (M = 1, every row count a compile-time 1) or kGemvMaxM (M = 2..4).
+// MR: 1 (M = 1, every row count a compile-time 1), kGemvMaxM (M = 2..4,
+// outputs in lanes 0-15) or 16 (M = 5..16, outputs in every lane).
 template <int B, int MODE, int MR>
 __global__ __launch_bounds__(64 * kGemvWaves) void linear_gemv_kernel(
     DevMatrix m, const uint16_t* __restrict__ x, int m_rows, uint16_t* __restrict__ y,
@@ -647,11 +648,19 @@ __global__ __launch_bounds__(64 * kGemvWaves) void linear_gemv_kernel(
     mul(b0, wave);
     mul(b1, wave + kGemvWaves);
 
-    // D[e][n] of activation row e < M sits in lane n < 16, element e
-    if (lane < kTileRows) {
+    // D[i][n] of activation row i sits in lane 16 (i / 4) + n, element i % 4
+    if constexpr (MR <= 4) {
+        if (lane < kTileRows) {
 #pragma unroll
-        for (int e = 0; e < MR; ++e) {
-            if (e < M) red[wave][e][lane] = acc[e];
+            for (int e = 0; e < MR; ++e) {
+                if (e < M) red[wave][e][lane] = acc[e];
+            }
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int i = 4 * quarter + e;
+            if (i < M) red[wave][i][nl] = acc[e];
         }
     }
     __syncthreads();
@@ -1665,24 +1674,42 @@ constexpr int kDecodeMaxM = 64;
 // decode kernel is 4-6% faster (14336 x 4096 b = 4: 8.3 against 8.7 us,
 // b = 7: 12.3 against 13.0).  Elsewhere the GEMV kernel is ahead by up to
 // 24% (1024 x 4096).
-template <int B, int MODE>
-inline bool gemv_takes(const DevMatrix& m) {
-    if (MODE == kModeW) return false;
+inline bool gemv_takes(const DevMatrix& m, int mode) {
+    if (mode == kModeW) return false;
     if (m.spr <= kGemvMaxSteps / 2 || m.spr > kGemvMaxSteps) return false;
-    if (MODE != kModeRaw && ((B == 11 && m.spr != kGemvMaxSteps) || (B <= 7 && m.rtiles > 256))) return false;
+    if (mode != kModeRaw && ((m.bits == 11 && m.spr != kGemvMaxSteps) || (m.bits <= 7 && m.rtiles > 256)))
+        return false;
     return true;
 }
 
-// Whether linear_gemv_kernel takes 2 <= M <= 4: the integer-code arithmetic
-// where it takes M = 1, except b = 11.  Measured on MI355X (us, decode
-// kernel -> GEMV kernel, b = 10, M = 2 / 4): 4096 x 4096 6.28 -> 5.79 /
-// 6.45 -> 5.96; 11008 x 4096 11.98 -> 11.64 / 12.57 -> 11.99; 14336 x 4096
-// 15.09 -> 14.41 / 15.54 -> 15.15; 4096 x 3072 5.42 -> 5.27 / 5.60 -> 5.44;
-// b = 9 at 11008 x 4096 M = 4 11.51 -> 11.19.  At b = 11 the two are even
-// (+-1%); raw fp16 (b = 16) is 1-2% slower there.
-template <int B, int MODE>
-inline bool gemv_rows_takes(const DevMatrix& m) {
-    return MODE == kModeQ && B != 11 && gemv_takes<B, MODE>(m);
+// Whether linear_gemv_kernel takes 2 <= M <= 16: the integer-code
+// arithmetic where it takes M = 1, except b = 11; above eight rows only at
+// K = 4096 (every wave holding two tiles).  Measured on MI355X (us, decode
+// kernel -> GEMV kernel, b = 10): 4096 x 4096 M = 2 6.28 -> 5.79, M = 4
+// 6.45 -> 5.96, M = 8 6.74 -> 6.24, M = 16 7.26 -> 6.99; 11008 x 4096 M = 4
+// 12.57 -> 11.99, M = 7 13.92 -> 13.05; 14336 x 4096 M = 2 15.09 -> 14.41;
+// 2048 x 4096 M = 16 6.20 -> 5.98; 4096 x 3072 M = 4 5.60 -> 5.44, M = 8
+// 5.87 -> 5.76 but M = 16 6.12 -> 6.37.  At b = 11 the two are even (+-1%);
+// raw fp16 (b = 16) is 1-2% slower at M = 2..4.
+inline bool gemv_rows_takes(int64_t M, const DevMatrix& m, int mode) {
+    if (mode != kModeQ || m.bits == 11 || !gemv_takes(m, mode)) return false;
+    return M <= 8 || m.spr == kGemvMaxSteps;
+}
+
+// The kernel a forward of M <= 16 activation rows takes on matrix m in a
+// launch of its own.  A multi-matrix launch fuses only matrices that all
+// take the same route, so each output equals its matrix's own forward.
+enum DecodeRoute { kRouteGemv1, kRouteGemv4, kRouteGemv16, kRouteRows, kRouteDecode };
+
+inline DecodeRoute decode_route(int64_t M, const DevMatrix& m, int mode, int xvec, int cus) {
+    if (M == 1 && xvec == 2 && gemv_takes(m, mode)) return kRouteGemv1;
+    if (decode_rows_per_workgroup(M, m, mode, cus) > 0) return kRouteRows;
+    if (M <= 16 && xvec == 2 && gemv_rows_takes(M, m, mode)) return M <= kGemvMaxM ? kRouteGemv4 : kRouteGemv16;
+    return kRouteDecode;
+}
+
+inline int linear_mode(int bits, bool exact_w16) {
+    return bits == 16 ? kModeRaw : (bits <= 12 && !exact_w16 ? kModeQ : kModeW);
 }
 
 // Whether the 256 x 256 prefill tiles finish before the 128 x 256 ones.
@@ -1833,19 +1860,41 @@ hipError_t run_linear_mode(const DevMatrix& m, const uint16_t* x, int64_t M, uin
     const uint64_t groups = static_cast<uint64_t>(m.rtiles) * m.spr * kTileSlots;
     const bool offsets32 = static_cast<uint64_t>(M) * m.cols * 2 < (uint64_t(1) << 32) &&
                            (MODE == kModeRaw || groups * 32u < (uint64_t(1) << 32));
-    if (M == 1 && xvec == 2 && gemv_takes<B, MODE>(m)) {
-        hipLaunchKernelGGL((linear_gemv_kernel<B, MODE, 1>), dim3(tiles), dim3(64 * kGemvWaves),
-                           static_cast<size_t>(kGemvWaves) * 2 * kTileGroups * kGroup * 2, s, m, x, 1, y, bias, mt);
-    } else if (M <= kGemvMaxM && xvec == 2 && gemv_rows_takes<B, MODE>(m)) {
-        hipLaunchKernelGGL((linear_gemv_kernel<B, MODE, kGemvMaxM>), dim3(tiles), dim3(64 * kGemvWaves),
-                           static_cast<size_t>(kGemvWaves) * M * 2 * kTileGroups * kGroup * 2, s, m, x,
-                           static_cast<int>(M), y, bias, mt);
-    } else if (const int rt = mt.count == 1 ? decode_rows_per_workgroup(M, m, MODE, device_cu_count()) : 0; rt > 0) {
-        return launch_decode_rows(m, MODE, rt, x, M, y, bias, xvec, s);
-    } else if (M <= 16 || (M <= kDecodeMaxM && (mt.count > 1 || prefer_decode(M, m, device_cu_count())))) {
-        if (M <= 16) {
-            launch_decode<B, MODE, 1>(m, x, M, y, bias, xvec, s, mt, tiles);
-        } else if (M <= 32) {
+    const size_t gemv_lds = static_cast<size_t>(kGemvWaves) * M * 2 * kTileGroups * kGroup * 2;
+    if (M <= 16) {
+        // a multi-matrix launch reaches here only when every matrix takes this route
+        switch (decode_route(M, m, MODE, xvec, device_cu_count())) {
+            case kRouteGemv1:
+                if constexpr (MODE != kModeW) {
+                    hipLaunchKernelGGL((linear_gemv_kernel<B, MODE, 1>), dim3(tiles), dim3(64 * kGemvWaves), gemv_lds,
+                                       s, m, x, 1, y, bias, mt);
+                    return hipGetLastError();
+                }
+                return hipErrorInvalidValue;
+            case kRouteGemv4:
+            case kRouteGemv16:
+                if constexpr (MODE == kModeQ && B != 11) {
+                    if (M <= kGemvMaxM) {
+                        hipLaunchKernelGGL((linear_gemv_kernel<B, MODE, kGemvMaxM>), dim3(tiles), dim3(64 * kGemvWaves),
+                                           gemv_lds, s, m, x, static_cast<int>(M), y, bias, mt);
+                    } else {
+                        hipLaunchKernelGGL((linear_gemv_kernel<B, MODE, 16>), dim3(tiles), dim3(64 * kGemvWaves),
+                                           gemv_lds, s, m, x, static_cast<int>(M), y, bias, mt);
+                    }
+                    return hipGetLastError();
+                }
+                return hipErrorInvalidValue;
+            case kRouteRows:
+                if (mt.count > 1) return hipErrorInvalidValue;
+                return launch_decode_rows(m, MODE, decode_rows_per_workgroup(M, m, MODE, device_cu_count()), x, M, y,
+                                          bias, xvec, s);
+            case kRouteDecode:
+                launch_decode<B, MODE, 1>(m, x, M, y, bias, xvec, s, mt, tiles);
+                return hipGetLastError();
+        }
+    }
+    if (M <= kDecodeMaxM && (mt.count > 1 || prefer_decode(M, m, device_cu_count()))) {
+        if (M <= 32) {
             launch_decode<B, MODE, 2>(m, x, M, y, bias, xvec, s, mt, tiles);
         } else if constexpr (kDecodeMaxM > 32) {
             launch_decode<B, MODE, 4>(m, x, M, y, bias, xvec, s, mt, tiles);
@@ -1950,14 +1999,18 @@ hipError_t launch_linear_multi(const DevMatrix* ms, int count, bool exact_w16, c
     for (int j = 1; j < count; ++j) {
         if (ms[j].cols != ms[0].cols || ms[j].bits != ms[0].bits) return hipErrorInvalidValue;
     }
-    // A matrix that its own forward sends to linear_decode_rows_kernel fills
-    // the device by itself; the group then runs per matrix, so that every
-    // output equals that forward's bit for bit.
+    // The group shares one launch only when each matrix's own forward takes
+    // the same kernel (and not linear_decode_rows_kernel, which fills the
+    // device with one matrix), so that every output equals that forward's
+    // bit for bit; otherwise it runs per matrix.
     bool fused = M <= kDecodeMaxM;
     const int cus = device_cu_count();
+    const int xvec = x_vector_mode(ms[0], x);
+    const int mode = linear_mode(ms[0].bits, exact_w16);
+    const DecodeRoute route = decode_route(M, ms[0], mode, xvec, cus);
     for (int j = 0; j < count && fused; ++j) {
-        const int mode = ms[j].bits == 16 ? kModeRaw : (ms[j].bits <= 12 && !exact_w16 ? kModeQ : kModeW);
-        fused = prefer_decode(M, ms[j], cus) && decode_rows_per_workgroup(M, ms[j], mode, cus) == 0;
+        fused = prefer_decode(M, ms[j], cus) &&
+                (M > 16 || (decode_route(M, ms[j], mode, xvec, cus) == route && route != kRouteRows));
     }
     if (!fused) {
         for (int j = 0; j < count; ++j) {
