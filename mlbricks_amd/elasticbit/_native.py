@@ -139,8 +139,24 @@ def _policy(value: str) -> int:
         raise ValueError("decodePolicy must be 'hardwareNative' or 'fullPrecision'") from None
 
 
-def stream_handle(device: torch.device | None = None) -> int:
+# torch's raw current-stream query costs ~0.1 us; building a Stream object
+# for the same answer costs ~2 us, which a decode loop pays per launch.
+_raw_current_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _device_index(device: torch.device | int | None) -> int:
+    if device is None:
+        return torch.cuda.current_device()
+    if isinstance(device, int):
+        return device
+    index = torch.device(device).index
+    return torch.cuda.current_device() if index is None else index
+
+
+def stream_handle(device: torch.device | int | None = None) -> int:
     """hipStream_t of torch's current stream on ``device`` (0 = legacy default)."""
+    if _raw_current_stream is not None:
+        return int(_raw_current_stream(_device_index(device)))
     return int(torch.cuda.current_stream(device).cuda_stream)
 
 
@@ -240,8 +256,8 @@ def forward_torch_multi(matrices: Sequence["RuntimeMatrix"], input: torch.Tensor
     handles = (ctypes.c_void_p * n)(*[m._h for m in mats])
     ys = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
     bptr = (ctypes.c_void_p * n)(*[b.data_ptr() if b is not None else None for b in bs])
-    with torch.cuda.device(x.device):
-        check(_lib.eb_forward_multi(handles, n, x.data_ptr(), rows_in, ys, bptr, stream_handle(x.device)))
+    # eb_forward_multi makes the matrices' device current for the launch
+    check(_lib.eb_forward_multi(handles, n, x.data_ptr(), rows_in, ys, bptr, stream_handle(props[0].device_index)))
     return outs
 
 
@@ -573,9 +589,9 @@ class RuntimeMatrix:
             b = bias.contiguous()
         if m == 0:
             return out
-        with torch.cuda.device(x.device):
-            check(_lib.eb_forward(self._h, x.data_ptr(), m, out.data_ptr(),
-                                  b.data_ptr() if b is not None else None, stream_handle(x.device)))
+        # eb_forward makes the matrix's device (checked equal to x's) current for the launch
+        check(_lib.eb_forward(self._h, x.data_ptr(), m, out.data_ptr(),
+                              b.data_ptr() if b is not None else None, stream_handle(p.device_index)))
         return out
 
     def _materializeTorch(self) -> torch.Tensor:

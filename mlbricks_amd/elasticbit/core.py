@@ -415,9 +415,10 @@ class _ElasticLinear(nn.Module):
         return ",".join(frozen) or "auto"
 
     def _bias_as(self, x: torch.Tensor) -> torch.Tensor | None:
-        if self.bias is None:
-            return None
-        return self.bias.to(device=x.device, dtype=x.dtype)
+        bias = self.bias
+        if bias is None or (bias.dtype == x.dtype and bias.device == x.device):
+            return bias
+        return bias.to(device=x.device, dtype=x.dtype)
 
     def _forwardNative(self, x: torch.Tensor) -> torch.Tensor:
         return self.matrix._native.forwardTorch(x, bias=self._bias_as(x))
@@ -441,6 +442,12 @@ class _ElasticLinear(nn.Module):
         phase = "decode" if rows <= DECODE_PHASE_ROWS else "prefill"
         owner = self._routeOwners[phase]
         xc = x.contiguous() if hip_ok else x
+        if hip_ok and self.backend == "auto" and not (torch.is_grad_enabled() and x.requires_grad):
+            # A route the planner already froze for this owner is what
+            # qualify_operator_once would return: skip its per-call set-up
+            # (a decode loop pays it on every launch).
+            if EXECUTION_PLANNER.frozen_route(owner, "elastic_linear") == "native":
+                return self._forwardNative(xc)
         route = EXECUTION_PLANNER.qualify_operator_once(
             owner, "elastic_linear", xc,
             {"native": lambda: self._forwardNative(xc), "pytorch": lambda: self._forwardPytorch(x)},

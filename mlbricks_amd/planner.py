@@ -277,6 +277,15 @@ class MLBricksExecutionPlanner:
         return {key: route for key, route in table.items() if route in ROUTES}
 
     @staticmethod
+    def frozen_route(owner: object, op: str, training: bool = False) -> str | None:
+        """The route frozen for ``op`` on ``owner``, or None: the answer
+        qualify_operator_once gives an auto owner once it has qualified,
+        without building its arguments."""
+        table = getattr(owner, _OWNER_ROUTES, None)
+        route = table.get((str(op), bool(training))) if isinstance(table, dict) else None
+        return route if route in ROUTES else None
+
+    @staticmethod
     def clear_owner_routes(owner: object) -> None:
         """Forget an owner's frozen auto decisions (planner.py:420-433)."""
         for name, empty in ((_OWNER_ROUTES, {}), (_OWNER_DETAILS, {}), (_OWNER_HOT, None)):

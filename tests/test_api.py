@@ -172,6 +172,12 @@ def test_qualify_benchmarks_then_freezes_fastest_route(monkeypatch):
                                           native_available=True, training=False, default_auto="native",
                                           warmup=0, trials=1, switch_margin=0.0)
     assert again == "pytorch"
+    # the cheap lookup _ElasticLinear.forward uses gives the same frozen answer
+    assert planner.frozen_route(owner, "unit_element") == "pytorch"
+    assert planner.frozen_route(owner, "unit_element", training=True) is None
+    assert planner.frozen_route(Owner(), "unit_element") is None
+    planner.clear_owner_routes(owner)
+    assert planner.frozen_route(owner, "unit_element") is None
 
 
 def test_qualify_hysteresis_keeps_default_inside_margin(monkeypatch):
