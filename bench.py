@@ -635,6 +635,25 @@ def bolt_decode(args) -> int:
         lin_us = us - head_us
         lines.append(f"| {label} | {us:.1f} | {1e6 / us:.0f} | {nbytes / lin_us / 1e3:.0f} over {lin_us:.1f} us |")
     lines.append(f"| {rows[2][0]} | {head_us:.1f} | - | {head_bytes / head_us / 1e3:.0f} (fp16 head) |")
+    # As a decode loop would run the fused token: issued from Python with
+    # nothing holding the GPU (the host's per-launch cost shows), and as one
+    # captured HIP graph replayed per token.
+    with torch.inference_mode():
+        for _ in range(3):
+            token_fused()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(200):
+            token_fused()
+        torch.cuda.synchronize()
+        eager_us = (time.perf_counter() - t0) / 200 * 1e6
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            token_fused()
+        graph_us = time_launches([graph.replay], tokens, 3, 97) / tokens * 1e3
+    log(f"  fused token issued from Python: {eager_us:.1f} us; as one HIP graph: {graph_us:.1f} us")
+    lines.append(f"| fused token issued from Python, GPU not held (wall clock) | {eager_us:.1f} | {1e6 / eager_us:.0f} | - |")
+    lines.append(f"| fused token as one captured HIP graph per token | {graph_us:.1f} | {1e6 / graph_us:.0f} | - |")
     print(f"configs[4] compressed Linears: widths {dict(sorted(widths.items()))}; "
           f"{nbytes:,} B of compressed Linears + {head_bytes:,} B fp16 head per token", flush=True)
     print("\n".join(lines), flush=True)
