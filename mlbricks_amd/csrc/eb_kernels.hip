@@ -442,6 +442,10 @@ __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
         }
     }
 
+    // The waits after the first weight batch count the loads issued after
+    // the activation staging: keep the scheduler from moving any above it.
+    __builtin_amdgcn_sched_barrier(0);
+
     // Steps past the end (steps % kBatch != 0) reload the last tile; they
     // meet zero activations, and raw fp16 weights, which could hold Inf or
     // NaN, are zeroed there.
@@ -619,6 +623,9 @@ __global__ __launch_bounds__(64 * kGemvWaves) void linear_gemv_kernel(
                                              (lds_void_ptr)(xw + 512 * k), 16, 0, 0);
         }
     }
+    // The wait below counts the weight loads issued after these: keep the
+    // scheduler from moving any of them above.
+    __builtin_amdgcn_sched_barrier(0);
     const size_t slot0 = static_cast<size_t>(tile) * steps * kTileSlots + lane;
     Bits b0, b1;
     b0.load(m, slot0 + static_cast<size_t>(min(wave, steps - 1)) * kTileSlots);
