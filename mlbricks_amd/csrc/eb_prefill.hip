@@ -80,6 +80,7 @@ __global__ __launch_bounds__(64 * kQWaves) void linear_prefill_pp_kernel(
     using Bits = GroupBits<B, MODE>;
     constexpr int GL = GroupLoads<B, MODE>::value;  // vector loads per group
     constexpr int D = ring_depth<B, MODE>();
+    constexpr bool kReadInGroup = MODE == kModeQ && B <= 10;   // see the slice order below
     __shared__ __attribute__((aligned(16))) uint8_t xs[kQLds];
 
     const int xcd = blockIdx.x & 7;
@@ -180,9 +181,15 @@ __global__ __launch_bounds__(64 * kQWaves) void linear_prefill_pp_kernel(
     // with D = 3; with D = 2 it is rn itself, filled with h + 1).
     //
     // Slice q, entered with A-low(q) read and B(q) decoded into set q % 2:
-    //   loads; read A-high(q); wait A-low(q); low MFMAs + decode B(q+1)
-    //   block 0; wait A-high(q); read A-low(q+1); high MFMAs + decode B(q+1)
-    //   block 1.
+    //   loads; wait A-low(q); low MFMAs with the reads of A-high(q) after
+    //   the first and the second of them + decode B(q+1) block 0; wait
+    //   A-high(q); read A-low(q+1); high MFMAs + decode B(q+1) block 1.
+    // The A-high reads issued from within the MFMA group keep their LDS
+    // latency off the wave's critical path: read ahead of the low MFMAs, in
+    // slices 1 and 3 the compiler joined their wait to that of A-low
+    // (14336 x 4096, M = 2048, same box: b = 10 214.8 -> 213.0 us, b = 8
+    // 203.3 -> 199.4, bit-identical).  At b = 11, whose decode is longer,
+    // that order measured 1% slower; there A-high is read ahead as before.
     // Slice 3 instead waits for the loads of half step h + 1, passes the
     // barrier and reads A-low of slice 0 of h + 1; its high MFMAs overlap
     // both decodes of that slice.
@@ -202,11 +209,27 @@ __global__ __launch_bounds__(64 * kQWaves) void linear_prefill_pp_kernel(
                 load_a(h + 2, Q);
             }
             __builtin_amdgcn_sched_barrier(0);
-            read_a(1, h, Q);
-            wait_lgkmcnt<2>();                     // A-low(q) landed
-            __builtin_amdgcn_sched_barrier(0);
-            mfma_half(0, SET);
-            if constexpr (Q < 3) decode_b(SET ^ 1, 0, Q + 1, rc);
+            if constexpr (kReadInGroup) {
+                wait_lgkmcnt<0>();                 // A-low(q) landed
+                __builtin_amdgcn_sched_barrier(0);
+                mfma_half(0, SET);
+                read_a(1, h, Q);
+                if constexpr (Q < 3) decode_b(SET ^ 1, 0, Q + 1, rc);
+                // order: MFMA, read, MFMA, read, MFMA, eight VALU, MFMA, the rest
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            } else {
+                read_a(1, h, Q);
+                wait_lgkmcnt<2>();                 // A-low(q) landed
+                __builtin_amdgcn_sched_barrier(0);
+                mfma_half(0, SET);
+                if constexpr (Q < 3) decode_b(SET ^ 1, 0, Q + 1, rc);
+            }
             __builtin_amdgcn_sched_barrier(0);
             wait_lgkmcnt<0>();                     // A-high(q) landed
             if constexpr (Q == 3) {
