@@ -242,10 +242,15 @@ int eb_packed_linear(const void* x, int x_dtype, int64_t M, const uint8_t* packe
  * picks the shape with the fewer estimated rounds over the GPU's compute
  * units; NARROW forces 128 x 256 tiles; WIDE forces 256 x 256 tiles with
  * four waves where M and rows are both at least 256, WIDE8 the same tiles
- * with eight waves.  Results agree within the output tolerance either way;
- * the sum order differs.  Process-wide, read at each launch. */
+ * with eight waves (when they end in a partial round of the compute units,
+ * part of the output runs as 192 x 256 tiles in a second launch where that
+ * is estimated faster), WIDE8_PLAIN eight waves on 256 x 256 tiles only,
+ * WIDE8_SHORT eight waves on 192 x 256 tiles only.  Results agree within the
+ * output tolerance between shapes and are bit-identical among the three
+ * eight-wave modes; the sum order differs otherwise.  Process-wide, read at
+ * each launch. */
 enum { EB_PREFILL_TILES_AUTO = 0, EB_PREFILL_TILES_NARROW = 1, EB_PREFILL_TILES_WIDE = 2,
-       EB_PREFILL_TILES_WIDE8 = 3 };
+       EB_PREFILL_TILES_WIDE8 = 3, EB_PREFILL_TILES_WIDE8_PLAIN = 4, EB_PREFILL_TILES_WIDE8_SHORT = 5 };
 int eb_set_prefill_tiles(int mode);
 
 /* ---- host codec (the packer inside the RuntimeMatrix constructors) --------- */

@@ -1105,8 +1105,10 @@ int eb_packed_linear(const void* x, int x_dtype, int64_t M, const uint8_t* packe
 int eb_set_prefill_tiles(int mode) {
     return guarded([&] {
         require(mode == EB_PREFILL_TILES_AUTO || mode == EB_PREFILL_TILES_NARROW || mode == EB_PREFILL_TILES_WIDE ||
-                    mode == EB_PREFILL_TILES_WIDE8,
-                "prefill tile mode must be auto (0), narrow (1), wide (2) or wide with eight waves (3)");
+                    mode == EB_PREFILL_TILES_WIDE8 || mode == EB_PREFILL_TILES_WIDE8_PLAIN ||
+                    mode == EB_PREFILL_TILES_WIDE8_SHORT,
+                "prefill tile mode must be auto (0), narrow (1), wide (2), wide with eight waves (3), "
+                "the same without round balancing (4) or 192-row tiles with eight waves (5)");
         ebk::set_prefill_tiles(mode);
     });
 }

@@ -154,15 +154,24 @@ hipError_t launch_analyze_widths_totals(const uint16_t* w, int N, int K, const u
                                         const float* max_abs, double* totals, hipStream_t stream);
 
 // Prefill tile shape: 0 auto, 1 128 x 256, 2 256 x 256 with four waves,
-// 3 256 x 256 with eight waves (process-wide).
+// 3 256 x 256 with eight waves, a partial last round balanced with 192 x 256
+// tiles where that is estimated faster, 4 the same without the balancing,
+// 5 192 x 256 tiles with eight waves throughout (process-wide).
+constexpr int kPrefillTilesWide8 = 3;
+constexpr int kPrefillTilesWide8Plain = 4;
+constexpr int kPrefillTilesWide8Short = 5;
 void set_prefill_tiles(int mode);
 
-// 256 x 256 prefill tiles with eight waves (eb_prefill.hip).  mode: 0
-// integer-code dot product (b <= 12), 1 decoded fp16 weights, 2 raw fp16
-// weights (b = 16).  Requires M >= 1, cols % 8 == 0, a 16-byte aligned x,
-// M * cols * 2 below 4 GiB and planes below 4 GiB.
+// 256 x 256 (and 192 x 256) prefill tiles with eight waves (eb_prefill.hip).
+// mode: 0 integer-code dot product (b <= 12), 1 decoded fp16 weights, 2 raw
+// fp16 weights (b = 16).  cus: the device's compute units; tiles_mode: the
+// set_prefill_tiles mode.  Requires M >= 1, cols % 8 == 0, a 16-byte
+// aligned x, M * cols * 2 below 4 GiB and planes below 4 GiB.
 hipError_t launch_prefill_pp(const DevMatrix& m, int mode, const uint16_t* x, int64_t M, uint16_t* y,
-                             const uint16_t* bias, hipStream_t stream);
+                             const uint16_t* bias, hipStream_t stream, int cus, int tiles_mode);
+// Estimated time of launch_prefill_pp's launches for M x rows, in full
+// rounds of 256 x 256 tiles over `cus` CUs.
+double prefill_pp_rounds(int64_t M, int rows, int cus, int tiles_mode);
 
 // Batched decode with several row tiles per workgroup (eb_decode_rows.hip).
 // decode_rows_per_workgroup: the row tiles per workgroup it takes for this

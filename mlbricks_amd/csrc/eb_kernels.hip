@@ -1719,24 +1719,7 @@ inline int linear_mode(int bits, bool exact_w16) {
     return bits == 16 ? kModeRaw : (bits <= 12 && !exact_w16 ? kModeQ : kModeW);
 }
 
-// Whether the 256 x 256 prefill tiles finish before the 128 x 256 ones.
-// Cost in rounds of 128 x 256 tiles over the CUs: a 256 x 256 tile takes
-// about 1.7 of them (measured on MI355X, 14336 x 4096 b = 10: 116 us per
-// wide round, 68 us per narrow round); the narrow kernel runs a last round
-// that would leave half the CUs idle as half tiles, at about two thirds of
-// a round.
 std::atomic<int> g_prefill_tiles{0};   // eb_set_prefill_tiles
-
-inline bool prefer_wide_tiles(int64_t M, int rows, int cus) {
-    const int mode = g_prefill_tiles.load(std::memory_order_relaxed);
-    if (mode != 0) return mode >= 2;
-    const int64_t wide = ((M + kWRows - 1) / kWRows) * ((rows + kWN - 1) / kWN);
-    const int64_t narrow = ((M + 127) / 128) * ((rows + kPN - 1) / kPN);
-    const double t_wide = 1.7 * static_cast<double>((wide + cus - 1) / cus);
-    const int64_t rem = narrow % cus;
-    const double t_narrow = static_cast<double>(narrow / cus) + (rem == 0 ? 0.0 : (2 * rem <= cus ? 0.67 : 1.0));
-    return t_wide < t_narrow;
-}
 
 // Whether 256 x 256 tiles run with eight waves (eb_prefill.hip) rather than
 // four.  Measured on MI355X, best of two interleaved runs after a 25 ms
@@ -1750,7 +1733,30 @@ inline bool prefer_wide_tiles(int64_t M, int rows, int cus) {
 template <int B, int MODE>
 inline bool prefill_eight_waves() {
     const int mode = g_prefill_tiles.load(std::memory_order_relaxed);
-    return mode == 3 || (mode == 0 && MODE == kModeQ && B >= 8 && B <= 11);
+    return mode >= kPrefillTilesWide8 || (mode == 0 && MODE == kModeQ && B >= 8 && B <= 11);
+}
+
+// Whether the 256 x 256 prefill tiles finish before the 128 x 256 ones.
+// Cost in rounds of 128 x 256 tiles over the CUs: a full round of 256 x 256
+// tiles takes about 1.7 of them (measured on MI355X, 14336 x 4096 b = 10:
+// 116 us per wide round, 68 us per narrow round); the narrow kernel runs a
+// last round that would leave half the CUs idle as half tiles, at about two
+// thirds of a round.  The eight-wave kernel's launches are costed by
+// prefill_pp_rounds (a sparse last round is cheaper than a full one, and
+// may be balanced with 192-row tiles); the four-wave kernel's by whole
+// rounds.
+template <int B, int MODE>
+inline bool prefer_wide_tiles(int64_t M, int rows, int cus) {
+    const int mode = g_prefill_tiles.load(std::memory_order_relaxed);
+    if (mode != 0) return mode >= 2;
+    const int64_t wide = ((M + kWRows - 1) / kWRows) * ((rows + kWN - 1) / kWN);
+    const int64_t narrow = ((M + 127) / 128) * ((rows + kPN - 1) / kPN);
+    const double wide_rounds = prefill_eight_waves<B, MODE>() ? prefill_pp_rounds(M, rows, cus, mode)
+                                                              : static_cast<double>((wide + cus - 1) / cus);
+    const double t_wide = 1.7 * wide_rounds;
+    const int64_t rem = narrow % cus;
+    const double t_narrow = static_cast<double>(narrow / cus) + (rem == 0 ? 0.0 : (2 * rem <= cus ? 0.67 : 1.0));
+    return t_wide < t_narrow;
 }
 
 // Tiles of linear_prefill_kernel with MI 32-row activation blocks: full
@@ -1909,8 +1915,11 @@ hipError_t run_linear_mode(const DevMatrix& m, const uint16_t* x, int64_t M, uin
     } else if (mt.count > 1) {
         return hipErrorInvalidValue;      // the launcher splits prefill per matrix
     } else if (xvec && offsets32 && M >= kWRows && m.rows >= kWN &&
-               prefer_wide_tiles(M, m.rows, device_cu_count())) {
-        if (prefill_eight_waves<B, MODE>()) return launch_prefill_pp(m, MODE, x, M, y, bias, s);
+               prefer_wide_tiles<B, MODE>(M, m.rows, device_cu_count())) {
+        if (prefill_eight_waves<B, MODE>()) {
+            return launch_prefill_pp(m, MODE, x, M, y, bias, s, device_cu_count(),
+                                     g_prefill_tiles.load(std::memory_order_relaxed));
+        }
         const int mblocks = static_cast<int>((M + kWRows - 1) / kWRows);
         const int nblocks = (m.rows + kWN - 1) / kWN;
         const int jobs = mblocks * nblocks;

@@ -52,12 +52,13 @@
 // runs at once share their activation and weight blocks in its L2.
 #include "eb_device.h"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace ebk {
 namespace {
 
-constexpr int kQRows = 256;                  // activation rows per workgroup
+constexpr int kQRows = 256;                  // activation rows per workgroup, at most
 constexpr int kQN = 256;                     // weight rows per workgroup
 constexpr int kQHalfRow = kPRow / 2;         // bytes per staged row of a half step
 constexpr int kQHalf = kQRows * kQHalfRow;   // bytes per half-stage (32 KB)
@@ -67,16 +68,37 @@ constexpr int kQLds = kQStages * kQHalf > kQRows * kQCPitch ? kQStages * kQHalf 
 constexpr int kQGroupM = 4;                  // activation blocks per tile-order group
 constexpr int kQWaves = 8;
 
+// The tiles of one launch: up to two rectangles of tiles, each walked
+// kQGroupM activation blocks at a time along its weight-row blocks.
+struct PPRect {
+    int m0;         // first activation row
+    int mblocks;    // activation blocks (of the kernel's tile height)
+    int nb0;        // first 256-row weight block
+    int nblocks;
+};
+struct PPGrid {
+    PPRect r[2];
+    int jobs0;      // tiles of r[0]; later jobs are r[1]'s
+    int njobs;
+    int per_xcd;    // jobs per XCD (workgroup i runs on XCD i % 8)
+};
+
 // Depth of the weight-bit register ring (see the pipeline above).
 template <int B, int MODE>
 constexpr int ring_depth() {
     return (MODE == kModeRaw || B > 12) ? 2 : 3;
 }
 
-template <int B, int MODE>
+// AB: 32-row activation blocks per wave, so 64 AB activation rows per tile
+// (AB = 4: 256 x 256 tiles; AB = 3: 192 x 256).  The low operand half holds
+// two blocks, the high half AB - 2.
+template <int B, int MODE, int AB>
 __global__ __launch_bounds__(64 * kQWaves) void linear_prefill_pp_kernel(
     DevMatrix m, const uint16_t* __restrict__ x, int M, uint16_t* __restrict__ y,
-    const uint16_t* __restrict__ bias, int mblocks, int nblocks, int njobs, int per_xcd) {
+    const uint16_t* __restrict__ bias, const PPGrid g) {
+    static_assert(AB == 3 || AB == 4, "three or four activation blocks per wave");
+    constexpr int kRows = 64 * AB;              // activation rows of a tile
+    constexpr int AH = AB - 2;                  // blocks of the high operand half
     using Bits = GroupBits<B, MODE>;
     constexpr int GL = GroupLoads<B, MODE>::value;  // vector loads per group
     constexpr int D = ring_depth<B, MODE>();
@@ -85,20 +107,23 @@ __global__ __launch_bounds__(64 * kQWaves) void linear_prefill_pp_kernel(
 
     const int xcd = blockIdx.x & 7;
     const int local = blockIdx.x >> 3;
-    const int job = xcd * per_xcd + local;
-    if (local >= per_xcd || job >= njobs) return;
-    const int group = job / (kQGroupM * nblocks);
-    const int within = job - group * kQGroupM * nblocks;
-    const int gm = min(kQGroupM, mblocks - group * kQGroupM);
+    int job = xcd * g.per_xcd + local;
+    if (local >= g.per_xcd || job >= g.njobs) return;
+    const bool second = job >= g.jobs0;
+    const PPRect rc = second ? g.r[1] : g.r[0];
+    if (second) job -= g.jobs0;
+    const int group = job / (kQGroupM * rc.nblocks);
+    const int within = job - group * kQGroupM * rc.nblocks;
+    const int gm = min(kQGroupM, rc.mblocks - group * kQGroupM);
     const int mb = group * kQGroupM + within % gm;
-    const int nb = within / gm;
-    const int m0 = mb * kQRows;
+    const int nb = rc.nb0 + within / gm;
+    const int m0 = rc.m0 + mb * kRows;
     const int n0 = nb * kQN;
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // 0 .. 7
     const int colg = wave & 3;          // weight rows n0 + 64 colg ..
-    const int mh = wave >> 2;           // activation rows m0 + 128 mh ..
+    const int mh = wave >> 2;           // activation rows m0 + 32 AB mh ..
     const int n32 = lane & 31;
     const int half = lane >> 5;
     const int steps = m.spr;
@@ -124,52 +149,54 @@ __global__ __launch_bounds__(64 * kQWaves) void linear_prefill_pp_kernel(
         }
     }
 
-    // A of half step h: wave w fills rows 32w .. 32w + 31 of half-stage
-    // h % 4, eight rows (1 KB) per instruction; lane l writes physical chunk
-    // l % 8 of row l / 8, which holds logical chunk (l % 8) ^ ((row >> 1) & 7).
+    // A of half step h: wave w fills rows 8 AB w .. 8 AB w + 8 AB - 1 of
+    // half-stage h % 4, eight rows (1 KB) per instruction; lane l writes
+    // physical chunk l % 8 of row l / 8, which holds logical chunk
+    // (l % 8) ^ ((row >> 1) & 7).  Instruction i starts at row R = 8 (AB w +
+    // i), so (row >> 1) & 7 = (4 ((R / 8) & 1) + l / 16) & 7.
     // The launcher guarantees cols % 8 == 0, a 16-byte aligned x and
     // M * cols * 2 below 4 GiB.
     int achunk[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) achunk[i] = 8 * ((lane & 7) ^ ((4 * i + (lane >> 4)) & 7));
-    const int arow0 = m0 + wave * 32 + (lane >> 3);
+    const int arow0 = m0 + wave * 8 * AB + (lane >> 3);
     const uint8_t* xb = reinterpret_cast<const uint8_t*>(x);
     auto load_a = [&](int h, int i) {
         const int k0 = min(h >> 1, steps - 1) * kPK + (h & 1) * (kPK / 2);
         const uint32_t row = static_cast<uint32_t>(min(arow0 + 8 * i, M - 1));
         const uint32_t off = 2u * (row * static_cast<uint32_t>(m.cols) +
-                                   static_cast<uint32_t>(min(k0 + achunk[i & 1], m.cols - 8)));
+                                   static_cast<uint32_t>(min(k0 + achunk[(wave * AB + i) & 1], m.cols - 8)));
         __builtin_amdgcn_global_load_lds(
-            xb + off, (lds_void_ptr)(xs + (h & 3) * kQHalf + (wave * 32 + 8 * i) * kQHalfRow), 16, 0, 0);
+            xb + off, (lds_void_ptr)(xs + (h & 3) * kQHalf + (wave * 8 * AB + 8 * i) * kQHalfRow), 16, 0, 0);
     };
     auto load_b = [&](Bits (&r)[2], int h, int j) {
         const uint32_t st = static_cast<uint32_t>(min(h >> 1, steps - 1));
         r[j].load32(m, slot0[j][h & 1] + st * kTileSlots);
     };
 
-    floatx16 acc[4][2];
+    floatx16 acc[AB][2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < AB; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    // Operands: A in two halves (hh) of two 32-row blocks, each half single-
-    // buffered; B double-buffered by set.  hh, set and q are constants at
-    // every call, so the arrays stay in registers.
+    // Operands: A in two halves (hh) of two and AB - 2 32-row blocks, each
+    // half single-buffered; B double-buffered by set.  hh, set and q are
+    // constants at every call, so the arrays stay in registers.
     half8 pa[2][2], pb[2][2];
     const int aswz = (n32 >> 1) & 7;
     auto read_a = [&](int hh, int h, int q) {
         const int chunk = (4 * half + q) ^ aswz;
-        const uint8_t* base = xs + (h & 3) * kQHalf + (128 * mh + 64 * hh + n32) * kQHalfRow + chunk * 16;
+        const uint8_t* base = xs + (h & 3) * kQHalf + (32 * AB * mh + 64 * hh + n32) * kQHalfRow + chunk * 16;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) pa[hh][i] = *reinterpret_cast<const half8*>(base + 32 * i * kQHalfRow);
+        for (int i = 0; i < (hh == 0 ? 2 : AH); ++i) pa[hh][i] = *reinterpret_cast<const half8*>(base + 32 * i * kQHalfRow);
     };
     auto decode_b = [&](int set, int j, int q, const Bits (&r)[2]) { pb[set][j] = r[j].operand(q, s[j]); };
     auto mfma_half = [&](int hh, int set) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < (hh == 0 ? 2 : AH); ++i)
 #pragma unroll
             for (int j = 0; j < 2; ++j)
                 acc[2 * hh + i][j] =
@@ -199,14 +226,14 @@ __global__ __launch_bounds__(64 * kQWaves) void linear_prefill_pp_kernel(
             constexpr int Q = decltype(q_c)::value;
             constexpr int SET = Q & 1;
             if constexpr (D == 3) {
-                load_a(h + 2, Q);
+                if constexpr (Q < AB) load_a(h + 2, Q);
                 if constexpr (Q < 2) load_b(rf, h + 2, Q);
             } else {
                 if constexpr (Q == 0) {
                     load_b(rf, h + 1, 0);
                     load_b(rf, h + 1, 1);
                 }
-                load_a(h + 2, Q);
+                if constexpr (Q < AB) load_a(h + 2, Q);
             }
             __builtin_amdgcn_sched_barrier(0);
             if constexpr (kReadInGroup) {
@@ -215,17 +242,17 @@ __global__ __launch_bounds__(64 * kQWaves) void linear_prefill_pp_kernel(
                 mfma_half(0, SET);
                 read_a(1, h, Q);
                 if constexpr (Q < 3) decode_b(SET ^ 1, 0, Q + 1, rc);
-                // order: MFMA, read, MFMA, read, MFMA, eight VALU, MFMA, the rest
+                // order: MFMA, read, MFMA, (read,) MFMA, eight VALU, MFMA, the rest
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                if constexpr (AH == 2) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             } else {
                 read_a(1, h, Q);
-                wait_lgkmcnt<2>();                 // A-low(q) landed
+                wait_lgkmcnt<AH>();                // A-low(q) landed
                 __builtin_amdgcn_sched_barrier(0);
                 mfma_half(0, SET);
                 if constexpr (Q < 3) decode_b(SET ^ 1, 0, Q + 1, rc);
@@ -234,10 +261,10 @@ __global__ __launch_bounds__(64 * kQWaves) void linear_prefill_pp_kernel(
             wait_lgkmcnt<0>();                     // A-high(q) landed
             if constexpr (Q == 3) {
                 // A and B of half step h + 1 landed: younger are this half
-                // step's four activation loads and, with D = 3, its two
+                // step's AB activation loads and, with D = 3, its two
                 // weight groups (with D = 2 its weight groups are the ones
                 // waited for, issued before its activation loads)
-                wait_vmcnt<D == 3 ? 4 + 2 * GL : 4>();
+                wait_vmcnt<D == 3 ? AB + 2 * GL : AB>();
                 barrier_after_wait();
                 __builtin_amdgcn_sched_barrier(0);
                 if (more) read_a(0, h + 1, 0);
@@ -266,11 +293,11 @@ __global__ __launch_bounds__(64 * kQWaves) void linear_prefill_pp_kernel(
     // prologue: A of half steps 0 and 1, weight bits of half step 0 (and 1
     // with D = 3)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) load_a(0, i);
+    for (int i = 0; i < AB; ++i) load_a(0, i);
 #pragma unroll
     for (int j = 0; j < 2; ++j) load_b(ring0, 0, j);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) load_a(1, i);
+    for (int i = 0; i < AB; ++i) load_a(1, i);
     if constexpr (D == 3) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) load_b(ring1, 1, j);
@@ -321,11 +348,11 @@ __global__ __launch_bounds__(64 * kQWaves) void linear_prefill_pp_kernel(
         if (bias) bn[j] = bias[n];
     }
     {
-        uint8_t* cw = xs + (128 * mh) * kQCPitch + colg * 128;
+        uint8_t* cw = xs + (32 * AB * mh) * kQCPitch + colg * 128;
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < AB; ++i)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     const int r = 32 * i + 8 * (e >> 2) + 4 * half + (e & 3);
@@ -337,7 +364,7 @@ __global__ __launch_bounds__(64 * kQWaves) void linear_prefill_pp_kernel(
     const bool yvec = (m.rows % 8 == 0) && (reinterpret_cast<uintptr_t>(y) % 16 == 0);
     const int chunk = threadIdx.x & 31;         // 16-byte chunk of a 512-byte row
 #pragma unroll 4
-    for (int it = 0; it < kQRows / (64 * kQWaves / 32); ++it) {
+    for (int it = 0; it < kRows / (64 * kQWaves / 32); ++it) {
         const int r = it * (64 * kQWaves / 32) + (threadIdx.x >> 5);
         const int gr = m0 + r;
         const int gn = n0 + chunk * 8;
@@ -356,47 +383,134 @@ __global__ __launch_bounds__(64 * kQWaves) void linear_prefill_pp_kernel(
     }
 }
 
+PPGrid pp_grid(const PPRect& a, const PPRect& b) {
+    PPGrid g{};
+    g.r[0] = a;
+    g.r[1] = b;
+    g.jobs0 = a.mblocks * a.nblocks;
+    g.njobs = g.jobs0 + b.mblocks * b.nblocks;
+    g.per_xcd = (g.njobs + 7) / 8;
+    return g;
+}
+
+// The launches of one prefill: 256 x 256 tiles (full) and 192 x 256 tiles
+// (short), either possibly empty, each one launch.
+//
+// Rounds.  Measured on MI355X (256 CUs), 14336 x 4096, b = 10, one launch of
+// one tile height, us by tiles in the launch:
+//   256-row tiles: 56: 78.9, 112: 80.0, 168: 93.0, 224: 110.8, 280: 192.0,
+//   336: 196.8, 392: 203.4, 448: 214.2, 504: 230.0;
+//   192-row tiles: 112: 70.3, 168: 79.6, 224: 90.3, 280: 160.9, 336: 163.4,
+//   392: 168.8, 448: 176.3, 504: 193.0, 560: 257.9
+// (b = 8 alike).  A round that keeps every CU busy is held by the chip as
+// a whole, a sparse one by each CU's own tile: a round with a fraction f of
+// the CUs busy costs about max(0.69, 0.45 + 0.55 f) of a full round of
+// 256-row tiles, and of 192-row tiles max(0.60, 0.44 + 0.39 f) (0.83 when
+// full).  So a 256 x 256 grid whose last round is sparse is better run as
+// whole rounds of 256 x 256 tiles plus 192 x 256 tiles for the rest: every
+// activation block of the first weight-row blocks and the first k of the
+// last n stay 256 x 256, the rest of those n columns becomes 192 x 256.
+// pp_plan picks k and n by that cost and takes the plan when it predicts at
+// least 3% less time than the plain grid (same box, us, plain -> plan:
+// 14336 x 4096 M = 1536 196.8 -> 175.5, 11008 x 4096 M = 2048 195.9 ->
+// 183.1; the model rejects M = 2048 at 14336 x 4096, measured 214.0 ->
+// 215.9).  Both tile shapes accumulate every output over K in the same
+// order, so the output does not depend on the plan.
+double pp_rounds_cost(int tiles, int cus, bool short_tiles) {
+    if (tiles <= 0) return 0.0;
+    const int whole = tiles / cus;
+    const int rem = tiles % cus;
+    const double f = static_cast<double>(rem) / cus;
+    double cost = whole * (short_tiles ? 0.83 : 1.0);
+    if (rem > 0) cost += short_tiles ? std::max(0.60, 0.44 + 0.39 * f) : std::max(0.69, 0.45 + 0.55 * f);
+    return cost;
+}
+
+struct PPPlan {
+    PPGrid full;
+    PPGrid short_tiles;
+    double cost;      // in full rounds of 256 x 256 tiles
+};
+
+PPPlan pp_plan(int64_t M64, int rows, int cus, int tiles_mode) {
+    const int M = static_cast<int>(M64);
+    const int mb = (M + kQRows - 1) / kQRows;
+    const int nb = (rows + kQN - 1) / kQN;
+    const PPRect none{0, 0, 0, 0};
+    PPPlan plan{pp_grid({0, mb, 0, nb}, none), pp_grid(none, none), pp_rounds_cost(mb * nb, cus, false)};
+    if (tiles_mode == kPrefillTilesWide8Short) {
+        const int sb = (M + 191) / 192;
+        plan.full = pp_grid(none, none);
+        plan.short_tiles = pp_grid({0, sb, 0, nb}, none);
+        plan.cost = pp_rounds_cost(sb * nb, cus, true);
+        return plan;
+    }
+    if (tiles_mode == kPrefillTilesWide8Plain || (mb * nb) % cus == 0) return plan;
+    double best = 0.97 * plan.cost;
+    for (int k = 0; k < mb; ++k) {                     // 256-row blocks kept in the mixed columns
+        const int s = (M - kQRows * k + 191) / 192;    // 192-row tiles below them
+        for (int n = 1; n <= nb; ++n) {                // mixed columns: the last n weight-row blocks
+            const int full = mb * (nb - n) + k * n;
+            const double cost = pp_rounds_cost(full, cus, false) + pp_rounds_cost(s * n, cus, true);
+            if (cost < best) {
+                best = cost;
+                plan.full = pp_grid({0, mb, 0, nb - n}, {0, k, nb - n, n});
+                plan.short_tiles = pp_grid({kQRows * k, s, nb - n, n}, none);
+                plan.cost = cost;
+            }
+        }
+    }
+    return plan;
+}
+
 template <int B, int MODE>
 hipError_t launch_pp(const DevMatrix& m, const uint16_t* x, int64_t M, uint16_t* y, const uint16_t* bias,
-                     hipStream_t s) {
-    const int mblocks = static_cast<int>((M + kQRows - 1) / kQRows);
-    const int nblocks = (m.rows + kQN - 1) / kQN;
-    const int jobs = mblocks * nblocks;
-    const int per_xcd = (jobs + 7) / 8;
-    hipLaunchKernelGGL((linear_prefill_pp_kernel<B, MODE>), dim3(8 * per_xcd), dim3(64 * kQWaves), 0, s, m, x,
-                       static_cast<int>(M), y, bias, mblocks, nblocks, jobs, per_xcd);
+                     hipStream_t s, int cus, int tiles_mode) {
+    const PPPlan plan = pp_plan(M, m.rows, cus, tiles_mode);
+    if (plan.full.njobs > 0) {
+        hipLaunchKernelGGL((linear_prefill_pp_kernel<B, MODE, 4>), dim3(8 * plan.full.per_xcd), dim3(64 * kQWaves),
+                           0, s, m, x, static_cast<int>(M), y, bias, plan.full);
+    }
+    if (plan.short_tiles.njobs > 0) {
+        hipLaunchKernelGGL((linear_prefill_pp_kernel<B, MODE, 3>), dim3(8 * plan.short_tiles.per_xcd),
+                           dim3(64 * kQWaves), 0, s, m, x, static_cast<int>(M), y, bias, plan.short_tiles);
+    }
     return hipGetLastError();
 }
 
 template <int B>
 hipError_t launch_pp_bits(const DevMatrix& m, int mode, const uint16_t* x, int64_t M, uint16_t* y,
-                          const uint16_t* bias, hipStream_t s) {
+                          const uint16_t* bias, hipStream_t s, int cus, int tiles_mode) {
     if constexpr (B <= 12) {
-        if (mode == kModeQ) return launch_pp<B, kModeQ>(m, x, M, y, bias, s);
+        if (mode == kModeQ) return launch_pp<B, kModeQ>(m, x, M, y, bias, s, cus, tiles_mode);
     }
-    if (mode == kModeW) return launch_pp<B, kModeW>(m, x, M, y, bias, s);
+    if (mode == kModeW) return launch_pp<B, kModeW>(m, x, M, y, bias, s, cus, tiles_mode);
     return hipErrorInvalidValue;
 }
 
 }  // namespace
 
+double prefill_pp_rounds(int64_t M, int rows, int cus, int tiles_mode) {
+    return pp_plan(M, rows, cus, tiles_mode).cost;
+}
+
 hipError_t launch_prefill_pp(const DevMatrix& m, int mode, const uint16_t* x, int64_t M, uint16_t* y,
-                             const uint16_t* bias, hipStream_t s) {
-    if (mode == kModeRaw) return launch_pp<8, kModeRaw>(m, x, M, y, bias, s);
+                             const uint16_t* bias, hipStream_t s, int cus, int tiles_mode) {
+    if (mode == kModeRaw) return launch_pp<8, kModeRaw>(m, x, M, y, bias, s, cus, tiles_mode);
     switch (m.bits) {
-        case 3: return launch_pp_bits<3>(m, mode, x, M, y, bias, s);
-        case 4: return launch_pp_bits<4>(m, mode, x, M, y, bias, s);
-        case 5: return launch_pp_bits<5>(m, mode, x, M, y, bias, s);
-        case 6: return launch_pp_bits<6>(m, mode, x, M, y, bias, s);
-        case 7: return launch_pp_bits<7>(m, mode, x, M, y, bias, s);
-        case 8: return launch_pp_bits<8>(m, mode, x, M, y, bias, s);
-        case 9: return launch_pp_bits<9>(m, mode, x, M, y, bias, s);
-        case 10: return launch_pp_bits<10>(m, mode, x, M, y, bias, s);
-        case 11: return launch_pp_bits<11>(m, mode, x, M, y, bias, s);
-        case 12: return launch_pp_bits<12>(m, mode, x, M, y, bias, s);
-        case 13: return launch_pp_bits<13>(m, mode, x, M, y, bias, s);
-        case 14: return launch_pp_bits<14>(m, mode, x, M, y, bias, s);
-        case 15: return launch_pp_bits<15>(m, mode, x, M, y, bias, s);
+        case 3: return launch_pp_bits<3>(m, mode, x, M, y, bias, s, cus, tiles_mode);
+        case 4: return launch_pp_bits<4>(m, mode, x, M, y, bias, s, cus, tiles_mode);
+        case 5: return launch_pp_bits<5>(m, mode, x, M, y, bias, s, cus, tiles_mode);
+        case 6: return launch_pp_bits<6>(m, mode, x, M, y, bias, s, cus, tiles_mode);
+        case 7: return launch_pp_bits<7>(m, mode, x, M, y, bias, s, cus, tiles_mode);
+        case 8: return launch_pp_bits<8>(m, mode, x, M, y, bias, s, cus, tiles_mode);
+        case 9: return launch_pp_bits<9>(m, mode, x, M, y, bias, s, cus, tiles_mode);
+        case 10: return launch_pp_bits<10>(m, mode, x, M, y, bias, s, cus, tiles_mode);
+        case 11: return launch_pp_bits<11>(m, mode, x, M, y, bias, s, cus, tiles_mode);
+        case 12: return launch_pp_bits<12>(m, mode, x, M, y, bias, s, cus, tiles_mode);
+        case 13: return launch_pp_bits<13>(m, mode, x, M, y, bias, s, cus, tiles_mode);
+        case 14: return launch_pp_bits<14>(m, mode, x, M, y, bias, s, cus, tiles_mode);
+        case 15: return launch_pp_bits<15>(m, mode, x, M, y, bias, s, cus, tiles_mode);
         default: return hipErrorInvalidValue;
     }
 }

@@ -218,7 +218,7 @@ def backendInfo() -> dict:
     }
 
 
-PREFILL_TILES = {"auto": 0, "narrow": 1, "wide": 2, "wide8": 3}
+PREFILL_TILES = {"auto": 0, "narrow": 1, "wide": 2, "wide8": 3, "wide8plain": 4, "wide8short": 5}
 
 
 def forward_torch_multi(matrices: Sequence["RuntimeMatrix"], input: torch.Tensor,
@@ -309,7 +309,10 @@ def width_errors_torch(weight: torch.Tensor, calibration16: torch.Tensor) -> tup
 def set_prefill_tiles(mode: str) -> None:
     """Tile shape of the prefill route (M > 16, b <= 15): 'auto' (default,
     picked by estimated rounds over the compute units), 'narrow' (128 x 256),
-    'wide' (256 x 256, four waves) or 'wide8' (256 x 256, eight waves).
+    'wide' (256 x 256, four waves), 'wide8' (256 x 256, eight waves, a
+    partial last round balanced with 192 x 256 tiles where estimated faster),
+    'wide8plain' (the same without the balancing) or 'wide8short' (192 x 256,
+    eight waves).
     Process-wide; a tuning and test control with no counterpart in the
     reference."""
     if mode not in PREFILL_TILES:

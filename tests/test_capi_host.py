@@ -277,7 +277,7 @@ def test_prefill_tile_mode_is_validated():
     with pytest.raises(ValueError, match="prefill tile mode"):
         native.set_prefill_tiles("square")
     lib = native.lib()
-    assert lib.eb_set_prefill_tiles(4) != 0
+    assert lib.eb_set_prefill_tiles(6) != 0
     assert lib.eb_set_prefill_tiles(-1) != 0
-    for mode in ("narrow", "wide", "wide8", "auto"):
+    for mode in ("narrow", "wide", "wide8", "wide8plain", "wide8short", "auto"):
         native.set_prefill_tiles(mode)
