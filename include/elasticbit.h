@@ -253,6 +253,17 @@ enum { EB_PREFILL_TILES_AUTO = 0, EB_PREFILL_TILES_NARROW = 1, EB_PREFILL_TILES_
        EB_PREFILL_TILES_WIDE8 = 3, EB_PREFILL_TILES_WIDE8_PLAIN = 4, EB_PREFILL_TILES_WIDE8_SHORT = 5 };
 int eb_set_prefill_tiles(int mode);
 
+/* Inspection (no counterpart in the reference): the launches of the
+ * eight-wave prefill kernel for an M x rows output on a device with `cus`
+ * compute units, under the current tile mode (EB_PREFILL_TILES_AUTO and
+ * WIDE8 plan alike).  rects receives three rectangles of five int32 each:
+ * first activation row, activation blocks, block height (256 or 192),
+ * first 256-row weight block, weight blocks.  The first two rectangles are
+ * the 256 x 256 launch, the third the 192 x 256 launch; unused ones are
+ * zero.  *cost (may be NULL) receives the plan's estimated time in full
+ * rounds of 256 x 256 tiles. */
+int eb_prefill_plan(int64_t M, int rows, int cus, int32_t* rects, double* cost);
+
 /* ---- host codec (the packer inside the RuntimeMatrix constructors) --------- */
 
 /* pack_exact_codes, runtime.cu:150-186.  payload_bytes must equal

@@ -1113,6 +1113,15 @@ int eb_set_prefill_tiles(int mode) {
     });
 }
 
+int eb_prefill_plan(int64_t M, int rows, int cus, int32_t* rects, double* cost) {
+    return guarded([&] {
+        require(M >= 1 && M <= 0x7fffffffLL && rows >= 1 && cus >= 1, "prefill plan: M, rows and cus must be positive");
+        require(rects != nullptr, "prefill plan: rects is null");
+        const double c = ebk::prefill_pp_plan_rects(M, rows, cus, ebk::prefill_tiles_mode(), rects);
+        if (cost) *cost = c;
+    });
+}
+
 int eb_host_pack_codes(const int16_t* codes, uint64_t count, int bits, uint8_t* payload, uint64_t payload_bytes) {
     return guarded([&] {
         require(codes && payload, "pack: null pointer");

@@ -172,6 +172,11 @@ hipError_t launch_prefill_pp(const DevMatrix& m, int mode, const uint16_t* x, in
 // Estimated time of launch_prefill_pp's launches for M x rows, in full
 // rounds of 256 x 256 tiles over `cus` CUs.
 double prefill_pp_rounds(int64_t M, int rows, int cus, int tiles_mode);
+// The same plan as rectangles of tiles (eb_prefill_plan's layout); returns
+// its estimated cost.
+double prefill_pp_plan_rects(int64_t M, int rows, int cus, int tiles_mode, int32_t* out);
+// The current set_prefill_tiles mode.
+int prefill_tiles_mode();
 
 // Batched decode with several row tiles per workgroup (eb_decode_rows.hip).
 // decode_rows_per_workgroup: the row tiles per workgroup it takes for this

@@ -1971,6 +1971,8 @@ hipError_t launch_repack(const uint8_t* canon, uint64_t canon_bytes, const DevMa
 
 void set_prefill_tiles(int mode) { g_prefill_tiles.store(mode, std::memory_order_relaxed); }
 
+int prefill_tiles_mode() { return g_prefill_tiles.load(std::memory_order_relaxed); }
+
 hipError_t launch_pack_codes(const int16_t* codes, uint64_t count, int bits, uint8_t* out, uint64_t out_bytes,
                              int* bad, hipStream_t stream) {
     return dispatch_bits<PackCodesOp>(bits, codes, count, out, out_bytes, bad, stream);

@@ -494,6 +494,19 @@ double prefill_pp_rounds(int64_t M, int rows, int cus, int tiles_mode) {
     return pp_plan(M, rows, cus, tiles_mode).cost;
 }
 
+double prefill_pp_plan_rects(int64_t M, int rows, int cus, int tiles_mode, int32_t* out) {
+    const PPPlan plan = pp_plan(M, rows, cus, tiles_mode);
+    const PPRect* rects[3] = {&plan.full.r[0], &plan.full.r[1], &plan.short_tiles.r[0]};
+    const int heights[3] = {kQRows, kQRows, 192};
+    const bool used[3] = {plan.full.jobs0 > 0, plan.full.njobs > plan.full.jobs0, plan.short_tiles.njobs > 0};
+    for (int i = 0; i < 3; ++i) {
+        const PPRect& r = *rects[i];
+        const int32_t v[5] = {r.m0, r.mblocks, heights[i], r.nb0, r.nblocks};
+        for (int j = 0; j < 5; ++j) out[5 * i + j] = used[i] ? v[j] : 0;
+    }
+    return plan.cost;
+}
+
 hipError_t launch_prefill_pp(const DevMatrix& m, int mode, const uint16_t* x, int64_t M, uint16_t* y,
                              const uint16_t* bias, hipStream_t s, int cus, int tiles_mode) {
     if (mode == kModeRaw) return launch_pp<8, kModeRaw>(m, x, M, y, bias, s, cus, tiles_mode);

@@ -103,6 +103,7 @@ _sig("eb_materialize_fp16", [_vp, _vp, _vp])
 _sig("eb_unpack_codes", [_vp, _vp, _vp])
 _sig("eb_packed_linear", [_vp, _i, _i64, _vp, _vp, _i, _vp, _i, _i64, _i64, _i64, _vp, _vp])
 _sig("eb_set_prefill_tiles", [_i])
+_sig("eb_prefill_plan", [ctypes.c_int64, _i, _i, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_double)])
 _sig("eb_host_pack_codes", [_i16p, _u64, _i, _u8p, _u64])
 _sig("eb_host_unpack_codes", [_u8p, _u64, _u64, _i, _i16p])
 
@@ -318,6 +319,20 @@ def set_prefill_tiles(mode: str) -> None:
     if mode not in PREFILL_TILES:
         raise ValueError(f"prefill tile mode must be one of {sorted(PREFILL_TILES)}")
     check(_lib.eb_set_prefill_tiles(PREFILL_TILES[mode]))
+
+
+def prefill_plan(M: int, rows: int, cus: int) -> tuple[list[tuple[int, int, int, int, int]], float]:
+    """The eight-wave prefill's launch plan for an M x rows output on `cus`
+    compute units under the current tile mode: rectangles of tiles (first
+    activation row, activation blocks, block height, first 256-row weight
+    block, weight blocks), 256-row ones first, and the estimated time in full
+    rounds of 256 x 256 tiles.  An inspection aid with no counterpart in the
+    reference."""
+    rects = (ctypes.c_int32 * 15)()
+    cost = ctypes.c_double()
+    check(_lib.eb_prefill_plan(M, rows, cus, rects, ctypes.byref(cost)))
+    out = [tuple(rects[5 * i:5 * i + 5]) for i in range(3)]
+    return [r for r in out if r[1] > 0 and r[4] > 0], cost.value
 
 
 def host_pack_codes(codes: np.ndarray, bits: int) -> np.ndarray:

@@ -281,3 +281,66 @@ def test_prefill_tile_mode_is_validated():
     assert lib.eb_set_prefill_tiles(-1) != 0
     for mode in ("narrow", "wide", "wide8", "wide8plain", "wide8short", "auto"):
         native.set_prefill_tiles(mode)
+
+
+def _plan_coverage(M, rows, cus):
+    """Every 64-row by 256-row block of the output below M is covered by
+    exactly one tile of the plan, and no tile starts at or beyond M."""
+    rects, cost = native.prefill_plan(M, rows, cus)
+    nb = (rows + 255) // 256
+    cells = np.zeros(((M + 63) // 64, nb), dtype=np.int32)
+    for m0, mblocks, height, nb0, nblocks in rects:
+        assert height in (256, 192) and m0 % 64 == 0
+        assert 0 <= nb0 and nb0 + nblocks <= nb
+        for i in range(mblocks):
+            r0 = m0 + i * height
+            assert r0 < M, (M, rows, cus, rects)
+            c0, c1 = r0 // 64, min(r0 + height, M + 63) // 64
+            cells[c0:min(c1, cells.shape[0]), nb0:nb0 + nblocks] += 1
+    assert (cells == 1).all(), (M, rows, cus, rects)
+    return rects, cost
+
+
+def test_prefill_plan_covers_every_output_once():
+    """The launch plan of the eight-wave prefill (host logic, no device):
+    whatever mix of 256 x 256 and 192 x 256 tiles it picks covers the output
+    exactly once, and its estimate never exceeds the plain grid's."""
+    try:
+        for cus in (256, 304, 80, 32):
+            for rows in (256, 1000, 4096, 11008, 14336, 30000):
+                for M in (256, 300, 1024, 1536, 1792, 2048, 2100, 3000, 4096, 8192):
+                    native.set_prefill_tiles("wide8")
+                    rects, cost = _plan_coverage(M, rows, cus)
+                    native.set_prefill_tiles("wide8plain")
+                    plain, plain_cost = _plan_coverage(M, rows, cus)
+                    assert len(plain) == 1 and plain[0][2] == 256
+                    assert cost <= plain_cost + 1e-12
+                    native.set_prefill_tiles("wide8short")
+                    short, _ = _plan_coverage(M, rows, cus)
+                    assert [r[2] for r in short] == [192]
+    finally:
+        native.set_prefill_tiles("auto")
+
+
+def test_prefill_plan_at_the_measured_shapes():
+    """The plan's choices at the shapes its cost model was measured on
+    (256 CUs): configs[3] keeps the plain 448-tile grid, 14336 x 4096 at
+    M = 1536 and 11008 x 4096 at M = 2048 balance their sparse last round."""
+    native.set_prefill_tiles("auto")
+    rects, _ = native.prefill_plan(2048, 14336, 256)
+    assert rects == [(0, 8, 256, 0, 56)]
+    for M, rows in ((1536, 14336), (2048, 11008)):
+        rects, cost = native.prefill_plan(M, rows, 256)
+        assert any(r[2] == 192 for r in rects), rects
+        full = sum(r[1] * r[4] for r in rects if r[2] == 256)
+        assert full <= 256
+    assert lib_rejects_bad_plan_arguments()
+
+
+def lib_rejects_bad_plan_arguments():
+    lib = native.lib()
+    rects = (ctypes.c_int32 * 15)()
+    assert lib.eb_prefill_plan(0, 4096, 256, rects, None) != 0
+    assert lib.eb_prefill_plan(256, 4096, 0, rects, None) != 0
+    assert lib.eb_prefill_plan(256, 4096, 256, None, None) != 0
+    return True
