@@ -703,7 +703,7 @@ def cpu_baseline(layer, seconds: float) -> dict:
     """The oracle's OpenMP GEMV (fp32 accumulate) over the same matrix and the
     same algorithmic bytes, on every core this process may use (bounded to
     ~`seconds`); beside it torch's fp32 F.linear on the CPU over the decoded
-    weights (BASELINE.md's secondary baseline)."""
+    weights, the secondary CPU baseline of the benchmark definition."""
     import numpy as np
     import torch
 
