@@ -641,7 +641,7 @@ def test_prefill_small_grids_match_decoded_product(native, rows, cols, M, b, pol
 
 
 @pytest.mark.parametrize("rows,cols,M,b,policy", [
-    (10240, 1000, 2048, 10, "hardwareNative"),    # 320 tiles: 256 of 256 rows, 88 of 192 (the last 128 rows)
+    (10240, 1000, 2048, 10, "hardwareNative"),    # 320 tiles of 256 rows; the plan runs 440 of 192 (the last 128 rows)
     (14336, 4096, 2048, 10, "hardwareNative"),    # configs[3]: 256 and 256
     (14336, 512, 1792, 8, "hardwareNative"),
     (9000, 640, 1600, 11, "fullPrecision"),       # ragged N, M = 6 x 256 + 64
@@ -660,10 +660,14 @@ def test_balanced_prefill_rounds_are_bit_identical(native, rows, cols, M, b, pol
     x = torch.from_numpy(rng.standard_normal((M, cols)).astype(np.float16)).cuda()
     bias = torch.from_numpy(rng.standard_normal(rows).astype(np.float16)).cuda()
     ys = {}
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
     try:
         for mode in ("wide8", "wide8plain", "wide8short"):
             native.set_prefill_tiles(mode)
             ys[mode] = m.forwardTorch(x, bias=bias)
+            if mode == "wide8" and (rows, M) == (10240, 2048) and cus == 256:
+                heights = {r[2] for r in native.prefill_plan(M, rows, cus)[0]}
+                assert 192 in heights, heights             # 192-row tiles ran in this launch
     finally:
         native.set_prefill_tiles("auto")
     assert torch.equal(ys["wide8"], ys["wide8plain"])
