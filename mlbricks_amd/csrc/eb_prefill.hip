@@ -463,10 +463,33 @@ PPPlan pp_plan(int64_t M64, int rows, int cus, int tiles_mode) {
     return plan;
 }
 
+// pp_plan searches k and n (tens of microseconds of host time for grids of
+// thousands of tiles); a launch asks for the plan twice (route choice and
+// launch), and a model asks for the same shapes again and again, so each host
+// thread keeps its last plans.
+PPPlan pp_plan_cached(int64_t M, int rows, int cus, int tiles_mode) {
+    struct Entry {
+        int64_t M;
+        int rows, cus, mode;
+        bool used;
+        PPPlan plan;
+    };
+    constexpr int kEntries = 16;
+    thread_local Entry cache[kEntries] = {};
+    thread_local int next = 0;
+    for (const Entry& e : cache) {
+        if (e.used && e.M == M && e.rows == rows && e.cus == cus && e.mode == tiles_mode) return e.plan;
+    }
+    const PPPlan plan = pp_plan(M, rows, cus, tiles_mode);
+    cache[next] = Entry{M, rows, cus, tiles_mode, true, plan};
+    next = (next + 1) % kEntries;
+    return plan;
+}
+
 template <int B, int MODE>
 hipError_t launch_pp(const DevMatrix& m, const uint16_t* x, int64_t M, uint16_t* y, const uint16_t* bias,
                      hipStream_t s, int cus, int tiles_mode) {
-    const PPPlan plan = pp_plan(M, m.rows, cus, tiles_mode);
+    const PPPlan plan = pp_plan_cached(M, m.rows, cus, tiles_mode);
     if (plan.full.njobs > 0) {
         hipLaunchKernelGGL((linear_prefill_pp_kernel<B, MODE, 4>), dim3(8 * plan.full.per_xcd), dim3(64 * kQWaves),
                            0, s, m, x, static_cast<int>(M), y, bias, plan.full);
@@ -491,11 +514,11 @@ hipError_t launch_pp_bits(const DevMatrix& m, int mode, const uint16_t* x, int64
 }  // namespace
 
 double prefill_pp_rounds(int64_t M, int rows, int cus, int tiles_mode) {
-    return pp_plan(M, rows, cus, tiles_mode).cost;
+    return pp_plan_cached(M, rows, cus, tiles_mode).cost;
 }
 
 double prefill_pp_plan_rects(int64_t M, int rows, int cus, int tiles_mode, int32_t* out) {
-    const PPPlan plan = pp_plan(M, rows, cus, tiles_mode);
+    const PPPlan plan = pp_plan_cached(M, rows, cus, tiles_mode);
     const PPRect* rects[3] = {&plan.full.r[0], &plan.full.r[1], &plan.short_tiles.r[0]};
     const int heights[3] = {kQRows, kQRows, 192};
     const bool used[3] = {plan.full.jobs0 > 0, plan.full.njobs > plan.full.jobs0, plan.short_tiles.njobs > 0};
