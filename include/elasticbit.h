@@ -242,21 +242,22 @@ int eb_packed_linear(const void* x, int x_dtype, int64_t M, const uint8_t* packe
  * picks the shape with the fewer estimated rounds over the GPU's compute
  * units; NARROW forces 128 x 256 tiles; WIDE forces 256 x 256 tiles with
  * four waves where M and rows are both at least 256, WIDE8 the same tiles
- * with eight waves (when they end in a partial round of the compute units,
- * part of the output runs as 192 x 256 tiles in a second launch where that
- * is estimated faster), WIDE8_PLAIN eight waves on 256 x 256 tiles only,
- * WIDE8_SHORT eight waves on 192 x 256 tiles only.  Results agree within the
- * output tolerance between shapes and are bit-identical among the three
- * eight-wave modes; the sum order differs otherwise.  Process-wide, read at
- * each launch. */
+ * with eight waves (for both, when the tiles end in a partial round of the
+ * compute units, part of the output runs as 192 x 256 tiles in a second
+ * launch where that is estimated faster); WIDE_PLAIN and WIDE8_PLAIN run
+ * 256 x 256 tiles only, WIDE_SHORT and WIDE8_SHORT 192 x 256 tiles only.
+ * Results agree within the output tolerance between shapes and are
+ * bit-identical among the modes of one wave count; the sum order differs
+ * otherwise.  Process-wide, read at each launch. */
 enum { EB_PREFILL_TILES_AUTO = 0, EB_PREFILL_TILES_NARROW = 1, EB_PREFILL_TILES_WIDE = 2,
-       EB_PREFILL_TILES_WIDE8 = 3, EB_PREFILL_TILES_WIDE8_PLAIN = 4, EB_PREFILL_TILES_WIDE8_SHORT = 5 };
+       EB_PREFILL_TILES_WIDE8 = 3, EB_PREFILL_TILES_WIDE8_PLAIN = 4, EB_PREFILL_TILES_WIDE8_SHORT = 5,
+       EB_PREFILL_TILES_WIDE_PLAIN = 6, EB_PREFILL_TILES_WIDE_SHORT = 7 };
 int eb_set_prefill_tiles(int mode);
 
 /* Inspection (no counterpart in the reference): the launches of the
- * eight-wave prefill kernel for an M x rows output on a device with `cus`
- * compute units, under the current tile mode (EB_PREFILL_TILES_AUTO and
- * WIDE8 plan alike).  rects receives three rectangles of five int32 each:
+ * 256 x 256 prefill kernels (four or eight waves) for an M x rows output on a
+ * device with `cus` compute units, under the current tile mode
+ * (EB_PREFILL_TILES_AUTO, WIDE and WIDE8 plan alike).  rects receives three rectangles of five int32 each:
  * first activation row, activation blocks, block height (256 or 192),
  * first 256-row weight block, weight blocks.  The first two rectangles are
  * the 256 x 256 launch, the third the 192 x 256 launch; unused ones are

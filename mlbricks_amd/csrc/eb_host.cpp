@@ -1106,9 +1106,11 @@ int eb_set_prefill_tiles(int mode) {
     return guarded([&] {
         require(mode == EB_PREFILL_TILES_AUTO || mode == EB_PREFILL_TILES_NARROW || mode == EB_PREFILL_TILES_WIDE ||
                     mode == EB_PREFILL_TILES_WIDE8 || mode == EB_PREFILL_TILES_WIDE8_PLAIN ||
-                    mode == EB_PREFILL_TILES_WIDE8_SHORT,
+                    mode == EB_PREFILL_TILES_WIDE8_SHORT || mode == EB_PREFILL_TILES_WIDE_PLAIN ||
+                    mode == EB_PREFILL_TILES_WIDE_SHORT,
                 "prefill tile mode must be auto (0), narrow (1), wide (2), wide with eight waves (3), "
-                "the same without round balancing (4) or 192-row tiles with eight waves (5)");
+                "the same without round balancing (4), 192-row tiles with eight waves (5), four-wave wide "
+                "tiles without round balancing (6) or 192-row tiles with four waves (7)");
         ebk::set_prefill_tiles(mode);
     });
 }

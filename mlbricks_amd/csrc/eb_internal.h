@@ -157,10 +157,39 @@ hipError_t launch_analyze_widths_totals(const uint16_t* w, int N, int K, const u
 // 3 256 x 256 with eight waves, a partial last round balanced with 192 x 256
 // tiles where that is estimated faster, 4 the same without the balancing,
 // 5 192 x 256 tiles with eight waves throughout (process-wide).
+constexpr int kPrefillTilesWide = 2;
 constexpr int kPrefillTilesWide8 = 3;
 constexpr int kPrefillTilesWide8Plain = 4;
 constexpr int kPrefillTilesWide8Short = 5;
+constexpr int kPrefillTilesWidePlain = 6;
+constexpr int kPrefillTilesWideShort = 7;
 void set_prefill_tiles(int mode);
+
+// The tiles of one launch of a 256 x 256 prefill kernel (four or eight
+// waves): up to two rectangles of tiles, each walked four activation blocks
+// at a time along its weight-row blocks.
+struct PrefillRect {
+    int m0;         // first activation row
+    int mblocks;    // activation blocks (of the launch's tile height)
+    int nb0;        // first 256-row weight block
+    int nblocks;
+};
+struct PrefillGrid {
+    PrefillRect r[2];
+    int jobs0;      // tiles of r[0]; later jobs are r[1]'s
+    int njobs;
+    int per_xcd;    // jobs per XCD (workgroup i runs on XCD i % 8)
+};
+// 256 x 256 tiles (full) and 192 x 256 tiles (short), each one launch,
+// either possibly empty; cost in full rounds of 256 x 256 tiles.
+struct PrefillPlan {
+    PrefillGrid full;
+    PrefillGrid short_tiles;
+    double cost;
+};
+// The plan for M x rows on `cus` CUs under a set_prefill_tiles mode
+// (eb_prefill.hip; cached per host thread).
+PrefillPlan prefill_plan(int64_t M, int rows, int cus, int tiles_mode);
 
 // 256 x 256 (and 192 x 256) prefill tiles with eight waves (eb_prefill.hip).
 // mode: 0 integer-code dot product (b <= 12), 1 decoded fp16 weights, 2 raw

@@ -1252,25 +1252,34 @@ constexpr int kWHalfRow = kPRow / 2;        // bytes per staged row of a half st
 constexpr int kWHalf = kWRows * kWHalfRow;  // bytes per half-stage (32 KB)
 constexpr int kWGroupM = 4;                 // activation blocks per tile-order group
 
-template <int B, int MODE>
+// AB: 32-row activation blocks of the tile (8: 256 x 256 tiles; 6: 192 x 256).
+// The low operand half holds four blocks, the high half AB - 4.
+template <int B, int MODE, int AB>
 __global__ __launch_bounds__(256) void linear_prefill_wide_kernel(
     DevMatrix m, const uint16_t* __restrict__ x, int M, uint16_t* __restrict__ y,
-    const uint16_t* __restrict__ bias, int mblocks, int nblocks, int njobs, int per_xcd) {
+    const uint16_t* __restrict__ bias, const PrefillGrid g) {
     static_assert(B <= kWideMaxBits, "width beyond the wide kernel's ring");
+    static_assert(AB == 8 || AB == 6, "six or eight activation blocks per tile");
+    constexpr int kRows = 32 * AB;              // activation rows of a tile
+    constexpr int AH = AB - 4;                  // blocks of the high operand half
+    constexpr int AL = kRows / 32;              // A loads per wave per half step (eight rows each)
     using Bits = GroupBits<B, MODE>;
     constexpr int GL = GroupLoads<B, MODE>::value;  // vector loads per group
     __shared__ __attribute__((aligned(16))) uint8_t xs[4 * kWHalf];
 
     const int xcd = blockIdx.x & 7;
     const int local = blockIdx.x >> 3;
-    const int job = xcd * per_xcd + local;
-    if (local >= per_xcd || job >= njobs) return;
-    const int group = job / (kWGroupM * nblocks);
-    const int within = job - group * kWGroupM * nblocks;
-    const int gm = min(kWGroupM, mblocks - group * kWGroupM);
+    int job = xcd * g.per_xcd + local;
+    if (local >= g.per_xcd || job >= g.njobs) return;
+    const bool second = job >= g.jobs0;
+    const PrefillRect rc = second ? g.r[1] : g.r[0];
+    if (second) job -= g.jobs0;
+    const int group = job / (kWGroupM * rc.nblocks);
+    const int within = job - group * kWGroupM * rc.nblocks;
+    const int gm = min(kWGroupM, rc.mblocks - group * kWGroupM);
     const int mb = group * kWGroupM + within % gm;
-    const int nb = within / gm;
-    const int m0 = mb * kWRows;
+    const int nb = rc.nb0 + within / gm;
+    const int m0 = rc.m0 + mb * kRows;
     const int n0 = nb * kWN;
 
     const int lane = threadIdx.x & 63;
@@ -1298,9 +1307,11 @@ __global__ __launch_bounds__(256) void linear_prefill_wide_kernel(
         }
     }
 
-    // A: half step h (columns 64*(h%2) .. +63 of step h/2) of all 256 rows
-    // goes global -> LDS into half-stage h % 4 (32 KB, rows of 128 B).
-    // Wave w fills rows 64w .. 64w + 63, eight rows (1 KB) per instruction;
+    // A: half step h (columns 64*(h%2) .. +63 of step h/2) of the tile's
+    // rows goes global -> LDS into half-stage h % 4 (rows of 128 B).
+    // Wave w fills rows 8 AL w .. 8 AL w + 8 AL - 1, eight rows (1 KB) per
+    // instruction (8 AL w is a multiple of 16, so the swizzle below depends
+    // on instruction i alone);
     // lane l writes physical chunk l%8 of row l/8, which holds logical chunk
     // (l%8) ^ ((row >> 1) & 7): with that swizzle the 16 rows read by lanes
     // 0..15 of an operand read land on distinct banks.  The launcher
@@ -1309,7 +1320,7 @@ __global__ __launch_bounds__(256) void linear_prefill_wide_kernel(
     int achunk[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) achunk[i] = 8 * ((lane & 7) ^ ((4 * i + (lane >> 4)) & 7));
-    const int arow0 = m0 + wave * 64 + (lane >> 3);
+    const int arow0 = m0 + wave * 8 * AL + (lane >> 3);
     const uint8_t* xb = reinterpret_cast<const uint8_t*>(x);
     auto load_a = [&](int h, int i) {
         const int k0 = min(h >> 1, steps - 1) * kPK + (h & 1) * (kPK / 2);
@@ -1317,7 +1328,7 @@ __global__ __launch_bounds__(256) void linear_prefill_wide_kernel(
         const uint32_t off = 2u * (row * static_cast<uint32_t>(m.cols) +
                                    static_cast<uint32_t>(min(k0 + achunk[i & 1], m.cols - 8)));
         __builtin_amdgcn_global_load_lds(
-            xb + off, (lds_void_ptr)(xs + (h & 3) * kWHalf + (wave * 64 + 8 * i) * kWHalfRow), 16, 0, 0);
+            xb + off, (lds_void_ptr)(xs + (h & 3) * kWHalf + (wave * 8 * AL + 8 * i) * kWHalfRow), 16, 0, 0);
     };
     // weight bits of half step h, block j, into ring buffer r
     auto load_b = [&](Bits (&r)[2], int h, int j) {
@@ -1325,16 +1336,16 @@ __global__ __launch_bounds__(256) void linear_prefill_wide_kernel(
         r[j].load32(m, slot0[j][h & 1] + st * kTileSlots);
     };
 
-    floatx16 acc[8][2];
+    floatx16 acc[AB][2];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < AB; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    // Operands.  The A operands of a slice are two halves of four row
-    // blocks; each half is single-buffered: the high half of slice q is read
+    // Operands.  The A operands of a slice are two halves of four and AB - 4
+    // row blocks; each half is single-buffered: the high half of slice q is read
     // while the low-half MFMAs run, the low half of slice q + 1 while the
     // high-half MFMAs run.  The B operands (two decoded blocks) are
     // double-buffered by set.  set, hh and q are constants at every call, so
@@ -1345,12 +1356,12 @@ __global__ __launch_bounds__(256) void linear_prefill_wide_kernel(
         const int chunk = (4 * half + q) ^ aswz;
         const uint8_t* base = xs + (h & 3) * kWHalf + (128 * hh + n32) * kWHalfRow + chunk * 16;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) pa[hh][i] = *reinterpret_cast<const half8*>(base + 32 * i * kWHalfRow);
+        for (int i = 0; i < (hh == 0 ? 4 : AH); ++i) pa[hh][i] = *reinterpret_cast<const half8*>(base + 32 * i * kWHalfRow);
     };
     auto decode_b = [&](int set, int j, int q, const Bits (&r)[2]) { pb[set][j] = r[j].operand(q, s[j]); };
     auto mfma_half = [&](int hh, int set) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < (hh == 0 ? 4 : AH); ++i)
 #pragma unroll
             for (int j = 0; j < 2; ++j)
                 acc[4 * hh + i][j] =
@@ -1379,11 +1390,13 @@ __global__ __launch_bounds__(256) void linear_prefill_wide_kernel(
             constexpr int Q = decltype(q_c)::value;
             constexpr int SET = Q & 1;
 #pragma unroll
-            for (int i = 0; i < 2; ++i) load_a(h + 2, 2 * Q + i);
+            for (int i = 0; i < 2; ++i) {
+                if (2 * Q + i < AL) load_a(h + 2, 2 * Q + i);
+            }
             if constexpr (Q < 2) load_b(rf, h + 2, Q);
             __builtin_amdgcn_sched_barrier(0);
             read_a(1, h, Q);
-            wait_lgkmcnt<4>();                     // A-low(q) landed
+            wait_lgkmcnt<AH>();                    // A-low(q) landed
             __builtin_amdgcn_sched_barrier(0);
             mfma_half(0, SET);
             if constexpr (Q < 3) decode_b(SET ^ 1, 0, Q + 1, rc);
@@ -1391,8 +1404,8 @@ __global__ __launch_bounds__(256) void linear_prefill_wide_kernel(
             wait_lgkmcnt<0>();                     // A-high(q) landed
             if constexpr (Q == 3) {
                 // A and B of half step h + 1 landed: the younger loads are
-                // the eight A loads and two B groups of this half step
-                wait_vmcnt<8 + 2 * GL>();
+                // the AL A loads and two B groups of this half step
+                wait_vmcnt<AL + 2 * GL>();
                 barrier_after_wait();
                 __builtin_amdgcn_sched_barrier(0);
                 if (more) read_a(0, h + 1, 0);
@@ -1420,11 +1433,11 @@ __global__ __launch_bounds__(256) void linear_prefill_wide_kernel(
     Bits ring0[2], ring1[2], ring2[2];
     // prologue: half steps 0 and 1 (A and B)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) load_a(0, i);
+    for (int i = 0; i < AL; ++i) load_a(0, i);
 #pragma unroll
     for (int j = 0; j < 2; ++j) load_b(ring0, 0, j);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) load_a(1, i);
+    for (int i = 0; i < AL; ++i) load_a(1, i);
 #pragma unroll
     for (int j = 0; j < 2; ++j) load_b(ring1, 1, j);
     wait_vmcnt<0>();
@@ -1472,12 +1485,13 @@ __global__ __launch_bounds__(256) void linear_prefill_wide_kernel(
     const int chunk = threadIdx.x & 31;         // 16-byte chunk of a 512-byte row
 #pragma unroll
     for (int pass = 0; pass < 2; ++pass) {
+        const int pass_blocks = pass == 0 ? 4 : AH;   // 32-row blocks staged in this pass
         if (pass > 0) __syncthreads();
         uint8_t* cw = xs + wave * 128;
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < pass_blocks; ++i)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     const int r = 32 * i + 8 * (e >> 2) + 4 * half + (e & 3);
@@ -1486,7 +1500,7 @@ __global__ __launch_bounds__(256) void linear_prefill_wide_kernel(
                 }
         __syncthreads();
 #pragma unroll 2
-        for (int it = 0; it < 16; ++it) {
+        for (int it = 0; it < 4 * pass_blocks; ++it) {
             const int r = it * 8 + (threadIdx.x >> 5);
             const int gr = m0 + pass * 128 + r;
             const int gn = n0 + chunk * 8;
@@ -1733,7 +1747,8 @@ std::atomic<int> g_prefill_tiles{0};   // eb_set_prefill_tiles
 template <int B, int MODE>
 inline bool prefill_eight_waves() {
     const int mode = g_prefill_tiles.load(std::memory_order_relaxed);
-    return mode >= kPrefillTilesWide8 || (mode == 0 && MODE == kModeQ && B >= 8 && B <= 11);
+    if (mode == kPrefillTilesWide8 || mode == kPrefillTilesWide8Plain || mode == kPrefillTilesWide8Short) return true;
+    return mode == 0 && MODE == kModeQ && B >= 8 && B <= 11;
 }
 
 // Whether the 256 x 256 prefill tiles finish before the 128 x 256 ones.
@@ -1741,19 +1756,15 @@ inline bool prefill_eight_waves() {
 // tiles takes about 1.7 of them (measured on MI355X, 14336 x 4096 b = 10:
 // 116 us per wide round, 68 us per narrow round); the narrow kernel runs a
 // last round that would leave half the CUs idle as half tiles, at about two
-// thirds of a round.  The eight-wave kernel's launches are costed by
-// prefill_pp_rounds (a sparse last round is cheaper than a full one, and
-// may be balanced with 192-row tiles); the four-wave kernel's by whole
-// rounds.
+// thirds of a round.  The 256 x 256 launches, four or eight waves, are
+// costed by prefill_pp_rounds: a sparse last round is cheaper than a full
+// one, and may be balanced with 192-row tiles.
 template <int B, int MODE>
 inline bool prefer_wide_tiles(int64_t M, int rows, int cus) {
     const int mode = g_prefill_tiles.load(std::memory_order_relaxed);
     if (mode != 0) return mode >= 2;
-    const int64_t wide = ((M + kWRows - 1) / kWRows) * ((rows + kWN - 1) / kWN);
     const int64_t narrow = ((M + 127) / 128) * ((rows + kPN - 1) / kPN);
-    const double wide_rounds = prefill_eight_waves<B, MODE>() ? prefill_pp_rounds(M, rows, cus, mode)
-                                                              : static_cast<double>((wide + cus - 1) / cus);
-    const double t_wide = 1.7 * wide_rounds;
+    const double t_wide = 1.7 * prefill_pp_rounds(M, rows, cus, mode);
     const int64_t rem = narrow % cus;
     const double t_narrow = static_cast<double>(narrow / cus) + (rem == 0 ? 0.0 : (2 * rem <= cus ? 0.67 : 1.0));
     return t_wide < t_narrow;
@@ -1920,12 +1931,18 @@ hipError_t run_linear_mode(const DevMatrix& m, const uint16_t* x, int64_t M, uin
             return launch_prefill_pp(m, MODE, x, M, y, bias, s, device_cu_count(),
                                      g_prefill_tiles.load(std::memory_order_relaxed));
         }
-        const int mblocks = static_cast<int>((M + kWRows - 1) / kWRows);
-        const int nblocks = (m.rows + kWN - 1) / kWN;
-        const int jobs = mblocks * nblocks;
-        const int per_xcd = (jobs + 7) / 8;
-        hipLaunchKernelGGL((linear_prefill_wide_kernel<B, MODE>), dim3(8 * per_xcd), dim3(256), 0, s, m, x,
-                           static_cast<int>(M), y, bias, mblocks, nblocks, jobs, per_xcd);
+        if constexpr (B <= kWideMaxBits) {
+            const PrefillPlan plan = prefill_plan(M, m.rows, device_cu_count(),
+                                                  g_prefill_tiles.load(std::memory_order_relaxed));
+            if (plan.full.njobs > 0) {
+                hipLaunchKernelGGL((linear_prefill_wide_kernel<B, MODE, 8>), dim3(8 * plan.full.per_xcd), dim3(256),
+                                   0, s, m, x, static_cast<int>(M), y, bias, plan.full);
+            }
+            if (plan.short_tiles.njobs > 0) {
+                hipLaunchKernelGGL((linear_prefill_wide_kernel<B, MODE, 6>), dim3(8 * plan.short_tiles.per_xcd),
+                                   dim3(256), 0, s, m, x, static_cast<int>(M), y, bias, plan.short_tiles);
+            }
+        }
     } else if (xvec && offsets32) {
         const int cus = device_cu_count();
         if (narrow_workgroups(M, m.rows, 4, cus) <= cus / 2) {

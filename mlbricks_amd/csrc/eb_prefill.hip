@@ -68,20 +68,9 @@ constexpr int kQLds = kQStages * kQHalf > kQRows * kQCPitch ? kQStages * kQHalf 
 constexpr int kQGroupM = 4;                  // activation blocks per tile-order group
 constexpr int kQWaves = 8;
 
-// The tiles of one launch: up to two rectangles of tiles, each walked
-// kQGroupM activation blocks at a time along its weight-row blocks.
-struct PPRect {
-    int m0;         // first activation row
-    int mblocks;    // activation blocks (of the kernel's tile height)
-    int nb0;        // first 256-row weight block
-    int nblocks;
-};
-struct PPGrid {
-    PPRect r[2];
-    int jobs0;      // tiles of r[0]; later jobs are r[1]'s
-    int njobs;
-    int per_xcd;    // jobs per XCD (workgroup i runs on XCD i % 8)
-};
+using PPRect = PrefillRect;
+using PPGrid = PrefillGrid;
+using PPPlan = PrefillPlan;
 
 // Depth of the weight-bit register ring (see the pipeline above).
 template <int B, int MODE>
@@ -426,26 +415,22 @@ double pp_rounds_cost(int tiles, int cus, bool short_tiles) {
     return cost;
 }
 
-struct PPPlan {
-    PPGrid full;
-    PPGrid short_tiles;
-    double cost;      // in full rounds of 256 x 256 tiles
-};
-
 PPPlan pp_plan(int64_t M64, int rows, int cus, int tiles_mode) {
     const int M = static_cast<int>(M64);
     const int mb = (M + kQRows - 1) / kQRows;
     const int nb = (rows + kQN - 1) / kQN;
     const PPRect none{0, 0, 0, 0};
     PPPlan plan{pp_grid({0, mb, 0, nb}, none), pp_grid(none, none), pp_rounds_cost(mb * nb, cus, false)};
-    if (tiles_mode == kPrefillTilesWide8Short) {
+    if (tiles_mode == kPrefillTilesWide8Short || tiles_mode == kPrefillTilesWideShort) {
         const int sb = (M + 191) / 192;
         plan.full = pp_grid(none, none);
         plan.short_tiles = pp_grid({0, sb, 0, nb}, none);
         plan.cost = pp_rounds_cost(sb * nb, cus, true);
         return plan;
     }
-    if (tiles_mode == kPrefillTilesWide8Plain || (mb * nb) % cus == 0) return plan;
+    if (tiles_mode == kPrefillTilesWide8Plain || tiles_mode == kPrefillTilesWidePlain || (mb * nb) % cus == 0) {
+        return plan;
+    }
     double best = 0.97 * plan.cost;
     for (int k = 0; k < mb; ++k) {                     // 256-row blocks kept in the mixed columns
         const int s = (M - kQRows * k + 191) / 192;    // 192-row tiles below them
@@ -512,6 +497,10 @@ hipError_t launch_pp_bits(const DevMatrix& m, int mode, const uint16_t* x, int64
 }
 
 }  // namespace
+
+PrefillPlan prefill_plan(int64_t M, int rows, int cus, int tiles_mode) {
+    return pp_plan_cached(M, rows, cus, tiles_mode);
+}
 
 double prefill_pp_rounds(int64_t M, int rows, int cus, int tiles_mode) {
     return pp_plan_cached(M, rows, cus, tiles_mode).cost;

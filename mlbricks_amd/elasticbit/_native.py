@@ -219,7 +219,8 @@ def backendInfo() -> dict:
     }
 
 
-PREFILL_TILES = {"auto": 0, "narrow": 1, "wide": 2, "wide8": 3, "wide8plain": 4, "wide8short": 5}
+PREFILL_TILES = {"auto": 0, "narrow": 1, "wide": 2, "wide8": 3, "wide8plain": 4, "wide8short": 5,
+                 "wideplain": 6, "wideshort": 7}
 
 
 def forward_torch_multi(matrices: Sequence["RuntimeMatrix"], input: torch.Tensor,
@@ -310,10 +311,10 @@ def width_errors_torch(weight: torch.Tensor, calibration16: torch.Tensor) -> tup
 def set_prefill_tiles(mode: str) -> None:
     """Tile shape of the prefill route (M > 16, b <= 15): 'auto' (default,
     picked by estimated rounds over the compute units), 'narrow' (128 x 256),
-    'wide' (256 x 256, four waves), 'wide8' (256 x 256, eight waves, a
-    partial last round balanced with 192 x 256 tiles where estimated faster),
-    'wide8plain' (the same without the balancing) or 'wide8short' (192 x 256,
-    eight waves).
+    'wide' (256 x 256, four waves) or 'wide8' (eight waves), each with a
+    partial last round balanced by 192 x 256 tiles where estimated faster,
+    'wideplain' / 'wide8plain' (without the balancing) or 'wideshort' /
+    'wide8short' (192 x 256 tiles throughout).
     Process-wide; a tuning and test control with no counterpart in the
     reference."""
     if mode not in PREFILL_TILES:
@@ -322,7 +323,7 @@ def set_prefill_tiles(mode: str) -> None:
 
 
 def prefill_plan(M: int, rows: int, cus: int) -> tuple[list[tuple[int, int, int, int, int]], float]:
-    """The eight-wave prefill's launch plan for an M x rows output on `cus`
+    """The 256 x 256 prefill launch plan for an M x rows output on `cus`
     compute units under the current tile mode: rectangles of tiles (first
     activation row, activation blocks, block height, first 256-row weight
     block, weight blocks), 256-row ones first, and the estimated time in full

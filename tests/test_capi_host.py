@@ -277,9 +277,9 @@ def test_prefill_tile_mode_is_validated():
     with pytest.raises(ValueError, match="prefill tile mode"):
         native.set_prefill_tiles("square")
     lib = native.lib()
-    assert lib.eb_set_prefill_tiles(6) != 0
+    assert lib.eb_set_prefill_tiles(8) != 0
     assert lib.eb_set_prefill_tiles(-1) != 0
-    for mode in ("narrow", "wide", "wide8", "wide8plain", "wide8short", "auto"):
+    for mode in ("narrow", "wide", "wide8", "wide8plain", "wide8short", "wideplain", "wideshort", "auto"):
         native.set_prefill_tiles(mode)
 
 
@@ -309,15 +309,16 @@ def test_prefill_plan_covers_every_output_once():
         for cus in (256, 304, 80, 32):
             for rows in (256, 1000, 4096, 11008, 14336, 30000):
                 for M in (256, 300, 1024, 1536, 1792, 2048, 2100, 3000, 4096, 8192):
-                    native.set_prefill_tiles("wide8")
-                    rects, cost = _plan_coverage(M, rows, cus)
-                    native.set_prefill_tiles("wide8plain")
-                    plain, plain_cost = _plan_coverage(M, rows, cus)
-                    assert len(plain) == 1 and plain[0][2] == 256
-                    assert cost <= plain_cost + 1e-12
-                    native.set_prefill_tiles("wide8short")
-                    short, _ = _plan_coverage(M, rows, cus)
-                    assert [r[2] for r in short] == [192]
+                    for waves in ("wide8", "wide"):
+                        native.set_prefill_tiles(waves)
+                        rects, cost = _plan_coverage(M, rows, cus)
+                        native.set_prefill_tiles(waves + "plain")
+                        plain, plain_cost = _plan_coverage(M, rows, cus)
+                        assert len(plain) == 1 and plain[0][2] == 256
+                        assert cost <= plain_cost + 1e-12
+                        native.set_prefill_tiles(waves + "short")
+                        short, _ = _plan_coverage(M, rows, cus)
+                        assert [r[2] for r in short] == [192]
     finally:
         native.set_prefill_tiles("auto")
 

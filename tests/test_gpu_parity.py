@@ -553,11 +553,11 @@ def test_legacy_packed_linear_dtypes_and_torch_op(native, dtype):
 # shapes hit: only half tiles (108 tiles), only whole tiles (204), and a mix
 # (308 = 256 whole + 52 split), each with a partial K step, in both the
 # integer-dot and the decoded-fp16 arithmetic.
-@pytest.fixture(params=["wide", "wide8", "wide8short"])
+@pytest.fixture(params=["wide", "wide8", "wideshort", "wide8short"])
 def wide_tiles(native, request):
-    """Force the 256 x 256 prefill tiles, with four and with eight waves, or
-    the eight-wave 192 x 256 tiles, for one test (the automatic choice takes
-    them only for large grids)."""
+    """Force the 256 x 256 prefill tiles or the 192 x 256 ones, with four
+    and with eight waves, for one test (the automatic choice takes them only
+    for large grids)."""
     native.set_prefill_tiles(request.param)
     yield
     native.set_prefill_tiles("auto")
@@ -640,19 +640,21 @@ def test_prefill_small_grids_match_decoded_product(native, rows, cols, M, b, pol
     _check_prefill_shape(native, rows, cols, M, b, policy)
 
 
+@pytest.mark.parametrize("waves", ["wide8", "wide"])
 @pytest.mark.parametrize("rows,cols,M,b,policy", [
     (10240, 1000, 2048, 10, "hardwareNative"),    # 320 tiles of 256 rows; the plan runs 440 of 192 (the last 128 rows)
-    (14336, 4096, 2048, 10, "hardwareNative"),    # configs[3]: 256 and 256
+    (14336, 4096, 2048, 10, "hardwareNative"),    # configs[3]: the plain grid
     (14336, 512, 1792, 8, "hardwareNative"),
     (9000, 640, 1600, 11, "fullPrecision"),       # ragged N, M = 6 x 256 + 64
+    (8192, 768, 2560, 12, "hardwareNative"),      # 256 tiles of 256 rows, then 192-row tiles
 ])
-def test_balanced_prefill_rounds_are_bit_identical(native, rows, cols, M, b, policy):
-    """The eight-wave prefill whose grid ends in a partial round of the
-    CUs runs part of the output as 192 x 256 tiles in a second launch.  Every
-    output is accumulated over K in the same order whatever tile holds it,
-    so the balanced launches, the plain 256 x 256 grid and 192 x 256 tiles
-    throughout give the same bits, and that output matches the decoded
-    product."""
+def test_balanced_prefill_rounds_are_bit_identical(native, rows, cols, M, b, policy, waves):
+    """The 256 x 256 prefill (four or eight waves) whose grid ends in a
+    partial round of the CUs runs part of the output as 192 x 256 tiles in a
+    second launch.  Every output is accumulated over K in the same order
+    whatever tile holds it, so the balanced launches, the plain 256 x 256
+    grid and 192 x 256 tiles throughout give the same bits, and that output
+    matches the decoded product."""
     rng = np.random.default_rng(rows + cols + M + b)
     q = _codes(rng, rows, cols, b)
     s = rng.uniform(0.002, 0.05, size=rows).astype(np.float32)
@@ -662,19 +664,19 @@ def test_balanced_prefill_rounds_are_bit_identical(native, rows, cols, M, b, pol
     ys = {}
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     try:
-        for mode in ("wide8", "wide8plain", "wide8short"):
-            native.set_prefill_tiles(mode)
-            ys[mode] = m.forwardTorch(x, bias=bias)
-            if mode == "wide8" and (rows, M) == (10240, 2048) and cus == 256:
+        for suffix in ("", "plain", "short"):
+            native.set_prefill_tiles(waves + suffix)
+            ys[suffix] = m.forwardTorch(x, bias=bias)
+            if suffix == "" and (rows, M) == (10240, 2048) and cus == 256:
                 heights = {r[2] for r in native.prefill_plan(M, rows, cus)[0]}
                 assert 192 in heights, heights             # 192-row tiles ran in this launch
     finally:
         native.set_prefill_tiles("auto")
-    assert torch.equal(ys["wide8"], ys["wide8plain"])
-    assert torch.equal(ys["wide8short"], ys["wide8plain"])
+    assert torch.equal(ys[""], ys["plain"])
+    assert torch.equal(ys["short"], ys["plain"])
     wd = m._materializeTorch().float()
     full = torch.matmul(x.float(), wd.T.contiguous()) + bias.float()
-    assert float((ys["wide8"].float() - full).abs().max() / full.abs().max()) <= TOL
+    assert float((ys[""].float() - full).abs().max() / full.abs().max()) <= TOL
 
 
 def _check_prefill_shape(native, rows, cols, M, b, policy):
