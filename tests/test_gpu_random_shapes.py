@@ -8,7 +8,8 @@ from L2; one, two or four 16-row blocks), the prefill kernel (64- and
 kernel for unaligned or ragged activations.  Every output is checked
 against the fp32 product of the decoded weights (the W16A16 formula, within
 the 2e-3 bound for every arithmetic), and a corner of it against the fp64
-oracle of the reference formula.
+oracle of the reference formula.  A second sweep draws large prefill shapes
+for the 256 x 256 kernels' launch plans.
 """
 from __future__ import annotations
 
@@ -89,3 +90,45 @@ def test_random_shape_matches_decoded_product(native, seed):
     ref_max = float(np.abs(ref).max())
     if ref_max > 0:
         assert float(np.abs(got - ref).max()) / ref_max <= TOL, (rows, cols, M, b, policy)
+
+
+def _large_case(seed: int):
+    rng = np.random.default_rng(5000 + seed)
+    rows = int(rng.integers(2200, 16500))
+    cols = int(rng.choice([256, 640, 1000, 1536]))
+    M = int(rng.integers(256, 3300))
+    b = int(rng.integers(3, 16))
+    policy = str(rng.choice(["hardwareNative", "fullPrecision"]))
+    waves = str(rng.choice(["wide", "wide8"]))
+    return rng, rows, cols, M, b, policy, waves
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_large_prefill_plans_are_bit_identical(native, seed):
+    """Seeded large prefill shapes through the 256 x 256 kernels: the launch
+    plan (whole rounds of 256 x 256 tiles, the rest as 192 x 256 tiles where
+    estimated faster), the plain 256 x 256 grid and 192 x 256 tiles
+    throughout give the same bits, covering the output once whatever plan the
+    shape draws; the result matches the decoded product."""
+    rng, rows, cols, M, b, policy, waves = _large_case(seed)
+    qm = (1 << (b - 1)) - 1
+    q = rng.integers(-qm, qm + 1, size=(rows, cols)).astype(np.int16)
+    s = (rng.uniform(0.002, 0.05, size=rows) * min(1.0, 127.0 / qm)).astype(np.float32)
+    m = native.RuntimeMatrix._compressSelectedCodes(q, s, b, 0.01, 0.0, decodePolicy=policy)
+    x = torch.from_numpy(rng.standard_normal((M, cols)).astype(np.float16)).cuda()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    ys = {}
+    try:
+        for suffix in ("", "plain", "short"):
+            native.set_prefill_tiles(waves + suffix)
+            ys[suffix] = m.forwardTorch(x)
+        plan, _ = native.prefill_plan(M, rows, cus)
+    finally:
+        native.set_prefill_tiles("auto")
+    case = (rows, cols, M, b, policy, waves, plan)
+    assert torch.equal(ys[""], ys["plain"]), case
+    assert torch.equal(ys["short"], ys["plain"]), case
+    wd = m._materializeTorch().float()
+    full = torch.matmul(x.float(), wd.T.contiguous())
+    err = float((ys[""].float() - full).abs().max() / full.abs().max().clamp_min(1e-30))
+    assert err <= TOL, (case, err)
