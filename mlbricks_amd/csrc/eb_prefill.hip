@@ -8,13 +8,18 @@
 // lane), counters on configs[3] (14336 x 4096, M = 2048, b = 10) showed the
 // matrix cores busy 47% of the cycles and the waves waiting on memory or
 // LDS results 47% of theirs: nothing else could issue while the only wave
-// of a SIMD waited.  Here wave w owns weight rows 64 (w % 4) .. + 63 (two
-// 32-row blocks) for activation rows 128 (w / 4) .. + 127 (four 32-row
-// blocks): 4 x 2 blocks of 32 x 32, 128 accumulator registers per lane, so
-// two waves fit a SIMD and one multiplies while the other waits.  The two
-// waves of a column group load and decode the same weight bits (the second
-// load hits the CU's L1); the activation reads from LDS are as many as with
-// four waves, since each wave reads only its own 128 rows.
+// of a SIMD waited.  Here every wave holds 128 accumulator registers per
+// lane, so two waves fit a SIMD and one multiplies while the other waits.
+// Two layouts (pp_weight_blocks):
+//  * two weight blocks per wave: wave w owns weight rows 64 (w % 4) .. + 63
+//    for activation rows 128 (w / 4) .. + 127, 4 x 2 blocks of 32 x 32.
+//    The two waves of a column group load and decode the same weight bits
+//    (the second load hits the CU's L1); each wave reads only its own 128
+//    activation rows from LDS;
+//  * one weight block per wave (b = 9..12): wave w owns weight rows
+//    32 w .. 32 w + 31 for all 256 activation rows, 8 x 1 blocks.  Each
+//    weight bit is loaded and decoded once; each wave reads every
+//    activation row from LDS.
 //
 // Per K step (128 columns = one plane tile) the CU moves 64 KB of
 // activations global -> LDS and 2 x 40 KB (b = 10) of weight bits global ->
@@ -78,16 +83,34 @@ constexpr int ring_depth() {
     return (MODE == kModeRaw || B > 12) ? 2 : 3;
 }
 
-// AB: 32-row activation blocks per wave, so 64 AB activation rows per tile
-// (AB = 4: 256 x 256 tiles; AB = 3: 192 x 256).  The low operand half holds
-// two blocks, the high half AB - 2.
+// Weight blocks per wave: 2 (wave w: weight rows 64 (w % 4) .. + 63 of
+// activation rows 32 AB (w / 4) .. + 32 AB - 1) or 1 (wave w: weight rows
+// 32 w .. 32 w + 31 of every activation row of the tile).  With one block a
+// workgroup loads and decodes each weight bit once instead of twice and
+// reads twice the activation operands from LDS.  Measured on MI355X
+// (14336 x 4096 M = 2048 unless stated, us, two blocks -> one): b = 8
+// 202.1 -> 205.5; b = 9 215.0 -> 212.4; b = 10 216.7 -> 215.8; b = 11
+// 248.7 -> 231.5, 4096^2 M = 8192 272.6 -> 251.5; b = 12 250.6 -> 235.0
+// (the four-wave kernel: 240.8).
+template <int B, int MODE>
+constexpr int pp_weight_blocks() {
+    return (MODE == kModeQ && B >= 9 && B <= 12) ? 1 : 2;
+}
+
+// AB: 32-row activation blocks per tile and weight-block column, so 64 AB
+// activation rows per tile (AB = 4: 256 x 256 tiles; AB = 3: 192 x 256).
+// A wave's activation blocks come in two operand halves: with two weight
+// blocks per wave, two and AB - 2 blocks of its 32 AB rows; with one, AB
+// and AB blocks of all 64 AB rows.
 template <int B, int MODE, int AB>
 __global__ __launch_bounds__(64 * kQWaves) void linear_prefill_pp_kernel(
     DevMatrix m, const uint16_t* __restrict__ x, int M, uint16_t* __restrict__ y,
     const uint16_t* __restrict__ bias, const PPGrid g) {
     static_assert(AB == 3 || AB == 4, "three or four activation blocks per wave");
     constexpr int kRows = 64 * AB;              // activation rows of a tile
-    constexpr int AH = AB - 2;                  // blocks of the high operand half
+    constexpr int JB = pp_weight_blocks<B, MODE>();   // 32-row weight blocks per wave
+    constexpr int AL = JB == 2 ? 2 : AB;        // activation blocks of the low operand half
+    constexpr int AH = JB == 2 ? AB - 2 : AB;   // blocks of the high operand half
     using Bits = GroupBits<B, MODE>;
     constexpr int GL = GroupLoads<B, MODE>::value;  // vector loads per group
     constexpr int D = ring_depth<B, MODE>();
@@ -111,20 +134,20 @@ __global__ __launch_bounds__(64 * kQWaves) void linear_prefill_pp_kernel(
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // 0 .. 7
-    const int colg = wave & 3;          // weight rows n0 + 64 colg ..
-    const int mh = wave >> 2;           // activation rows m0 + 32 AB mh ..
+    const int colg = JB == 2 ? wave & 3 : wave;   // weight rows n0 + 32 JB colg ..
+    const int mh = JB == 2 ? wave >> 2 : 0;       // activation rows m0 + 32 AB mh ..
     const int n32 = lane & 31;
     const int half = lane >> 5;
     const int steps = m.spr;
-    const int nw0 = n0 + colg * 64;
+    const int nw0 = n0 + colg * 32 * JB;
 
     // B slots [j][p]: 32-row block j (row tiles nw0/16 + 2j, +1), group pair
     // p; lane (n32, half) holds group 2p + half of its row, whose codes
     // 8q .. 8q + 7 are the operand of slice q.
-    uint32_t slot0[2][2];
-    float s[2];
+    uint32_t slot0[JB][2];
+    float s[JB];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < JB; ++j) {
         const int rt = min(nw0 / kTileRows + 2 * j + (n32 >> 4), m.rtiles - 1);
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
@@ -158,38 +181,38 @@ __global__ __launch_bounds__(64 * kQWaves) void linear_prefill_pp_kernel(
         __builtin_amdgcn_global_load_lds(
             xb + off, (lds_void_ptr)(xs + (h & 3) * kQHalf + (wave * 8 * AB + 8 * i) * kQHalfRow), 16, 0, 0);
     };
-    auto load_b = [&](Bits (&r)[2], int h, int j) {
+    auto load_b = [&](Bits (&r)[JB], int h, int j) {
         const uint32_t st = static_cast<uint32_t>(min(h >> 1, steps - 1));
         r[j].load32(m, slot0[j][h & 1] + st * kTileSlots);
     };
 
-    floatx16 acc[AB][2];
+    floatx16 acc[AL + AH][JB];
 #pragma unroll
-    for (int i = 0; i < AB; ++i)
+    for (int i = 0; i < AL + AH; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < JB; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    // Operands: A in two halves (hh) of two and AB - 2 32-row blocks, each
-    // half single-buffered; B double-buffered by set.  hh, set and q are
+    // Operands: A in two halves (hh) of AL and AH 32-row blocks, each half
+    // single-buffered; B double-buffered by set.  hh, set and q are
     // constants at every call, so the arrays stay in registers.
-    half8 pa[2][2], pb[2][2];
+    half8 pa[2][AL], pb[2][JB];
     const int aswz = (n32 >> 1) & 7;
     auto read_a = [&](int hh, int h, int q) {
         const int chunk = (4 * half + q) ^ aswz;
-        const uint8_t* base = xs + (h & 3) * kQHalf + (32 * AB * mh + 64 * hh + n32) * kQHalfRow + chunk * 16;
+        const uint8_t* base = xs + (h & 3) * kQHalf + (32 * AB * mh + 32 * AL * hh + n32) * kQHalfRow + chunk * 16;
 #pragma unroll
-        for (int i = 0; i < (hh == 0 ? 2 : AH); ++i) pa[hh][i] = *reinterpret_cast<const half8*>(base + 32 * i * kQHalfRow);
+        for (int i = 0; i < (hh == 0 ? AL : AH); ++i) pa[hh][i] = *reinterpret_cast<const half8*>(base + 32 * i * kQHalfRow);
     };
-    auto decode_b = [&](int set, int j, int q, const Bits (&r)[2]) { pb[set][j] = r[j].operand(q, s[j]); };
+    auto decode_b = [&](int set, int j, int q, const Bits (&r)[JB]) { pb[set][j] = r[j].operand(q, s[j]); };
     auto mfma_half = [&](int hh, int set) {
 #pragma unroll
-        for (int i = 0; i < (hh == 0 ? 2 : AH); ++i)
+        for (int i = 0; i < (hh == 0 ? AL : AH); ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-                acc[2 * hh + i][j] =
-                    __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[hh][i], pb[set][j], acc[2 * hh + i][j], 0, 0, 0);
+            for (int j = 0; j < JB; ++j)
+                acc[AL * hh + i][j] =
+                    __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[hh][i], pb[set][j], acc[AL * hh + i][j], 0, 0, 0);
     };
 
     // Half step h.  rc: its weight bits; rn: those of h + 1 (decoded at the
@@ -209,18 +232,18 @@ __global__ __launch_bounds__(64 * kQWaves) void linear_prefill_pp_kernel(
     // Slice 3 instead waits for the loads of half step h + 1, passes the
     // barrier and reads A-low of slice 0 of h + 1; its high MFMAs overlap
     // both decodes of that slice.
-    auto half_step = [&](const Bits (&rc)[2], const Bits (&rn)[2], Bits (&rf)[2], int h) {
+    auto half_step = [&](const Bits (&rc)[JB], const Bits (&rn)[JB], Bits (&rf)[JB], int h) {
         const bool more = h + 1 < 2 * steps;
         auto slice = [&](auto q_c) {
             constexpr int Q = decltype(q_c)::value;
             constexpr int SET = Q & 1;
             if constexpr (D == 3) {
                 if constexpr (Q < AB) load_a(h + 2, Q);
-                if constexpr (Q < 2) load_b(rf, h + 2, Q);
+                if constexpr (Q < JB) load_b(rf, h + 2, Q);
             } else {
                 if constexpr (Q == 0) {
-                    load_b(rf, h + 1, 0);
-                    load_b(rf, h + 1, 1);
+#pragma unroll
+                    for (int j = 0; j < JB; ++j) load_b(rf, h + 1, j);
                 }
                 if constexpr (Q < AB) load_a(h + 2, Q);
             }
@@ -231,14 +254,24 @@ __global__ __launch_bounds__(64 * kQWaves) void linear_prefill_pp_kernel(
                 mfma_half(0, SET);
                 read_a(1, h, Q);
                 if constexpr (Q < 3) decode_b(SET ^ 1, 0, Q + 1, rc);
-                // order: MFMA, read, MFMA, (read,) MFMA, eight VALU, MFMA, the rest
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                if constexpr (AH == 2) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if constexpr (JB == 2) {
+                    // order: MFMA, read, MFMA, (read,) MFMA, eight VALU, MFMA, the rest
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    if constexpr (AH == 2) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                } else {
+                    // order: MFMA, read, ... (AB of each), eight VALU, the rest
+#pragma unroll
+                    for (int k = 0; k < AB; ++k) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    }
+                    __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+                }
             } else {
                 read_a(1, h, Q);
                 wait_lgkmcnt<AH>();                // A-low(q) landed
@@ -250,10 +283,10 @@ __global__ __launch_bounds__(64 * kQWaves) void linear_prefill_pp_kernel(
             wait_lgkmcnt<0>();                     // A-high(q) landed
             if constexpr (Q == 3) {
                 // A and B of half step h + 1 landed: younger are this half
-                // step's AB activation loads and, with D = 3, its two
+                // step's AB activation loads and, with D = 3, its JB
                 // weight groups (with D = 2 its weight groups are the ones
                 // waited for, issued before its activation loads)
-                wait_vmcnt<D == 3 ? AB + 2 * GL : AB>();
+                wait_vmcnt<D == 3 ? AB + JB * GL : AB>();
                 barrier_after_wait();
                 __builtin_amdgcn_sched_barrier(0);
                 if (more) read_a(0, h + 1, 0);
@@ -263,11 +296,11 @@ __global__ __launch_bounds__(64 * kQWaves) void linear_prefill_pp_kernel(
             __builtin_amdgcn_sched_barrier(0);
             mfma_half(1, SET);
             if constexpr (Q < 3) {
-                decode_b(SET ^ 1, 1, Q + 1, rc);
+                if constexpr (JB == 2) decode_b(SET ^ 1, 1, Q + 1, rc);
             } else {
                 if (more) {
-                    decode_b(0, 0, 0, rn);
-                    decode_b(0, 1, 0, rn);
+#pragma unroll
+                    for (int j = 0; j < JB; ++j) decode_b(0, j, 0, rn);
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -278,33 +311,33 @@ __global__ __launch_bounds__(64 * kQWaves) void linear_prefill_pp_kernel(
         slice(std::integral_constant<int, 3>{});
     };
 
-    Bits ring0[2], ring1[2], ring2[2];
+    Bits ring0[JB], ring1[JB], ring2[JB];
     // prologue: A of half steps 0 and 1, weight bits of half step 0 (and 1
     // with D = 3)
 #pragma unroll
     for (int i = 0; i < AB; ++i) load_a(0, i);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) load_b(ring0, 0, j);
+    for (int j = 0; j < JB; ++j) load_b(ring0, 0, j);
 #pragma unroll
     for (int i = 0; i < AB; ++i) load_a(1, i);
     if constexpr (D == 3) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) load_b(ring1, 1, j);
+        for (int j = 0; j < JB; ++j) load_b(ring1, 1, j);
     }
     wait_vmcnt<0>();
     barrier_after_wait();
     read_a(0, 0, 0);
-    decode_b(0, 0, 0, ring0);
-    decode_b(0, 1, 0, ring0);
+#pragma unroll
+    for (int j = 0; j < JB; ++j) decode_b(0, j, 0, ring0);
     if constexpr (D == 3) {
         // One step (two half steps) per iteration; the ring advances by two
         // buffers, (r0, r1, r2) <- (r2, r0, r1), by register copies.
         for (int st = 0; st < steps; ++st) {
             half_step(ring0, ring1, ring2, 2 * st);
             half_step(ring1, ring2, ring0, 2 * st + 1);
-            Bits t[2];
+            Bits t[JB];
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
+            for (int j = 0; j < JB; ++j) {
                 t[j].copy_from(ring0[j]);
                 ring0[j].copy_from(ring2[j]);
                 ring2[j].copy_from(ring1[j]);
@@ -326,10 +359,10 @@ __global__ __launch_bounds__(64 * kQWaves) void linear_prefill_pp_kernel(
     wait_vmcnt<0>();
     __syncthreads();
     static_assert(kQRows * kQCPitch <= kQLds, "output staging exceeds the LDS");
-    float sn[2];
-    uint16_t bn[2];
+    float sn[JB];
+    uint16_t bn[JB];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < JB; ++j) {
         const int n = min(nw0 + 32 * j + n32, m.rows - 1);
         sn[j] = 1.0f;
         bn[j] = 0;
@@ -337,11 +370,11 @@ __global__ __launch_bounds__(64 * kQWaves) void linear_prefill_pp_kernel(
         if (bias) bn[j] = bias[n];
     }
     {
-        uint8_t* cw = xs + (32 * AB * mh) * kQCPitch + colg * 128;
+        uint8_t* cw = xs + (32 * AB * mh) * kQCPitch + colg * 64 * JB;
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < JB; ++j)
 #pragma unroll
-            for (int i = 0; i < AB; ++i)
+            for (int i = 0; i < AL + AH; ++i)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     const int r = 32 * i + 8 * (e >> 2) + 4 * half + (e & 3);
