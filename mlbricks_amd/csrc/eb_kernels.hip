@@ -1740,16 +1740,16 @@ std::atomic<int> g_prefill_tiles{0};   // eb_set_prefill_tiles
 // warm-up (us, four -> eight waves): integer-code widths 8..11 gain
 // (14336 x 4096 M = 2048 b = 10 218.6 -> 215.2, b = 9 212.7 -> 211.0,
 // b = 8 209.5 -> 203.3; 4096 x 4096 M = 8192 b = 10 238.3 -> 236.6;
-// 14336 x 4096 M = 4096 b = 10 443.0 -> 427.4); b = 7 loses (214.3 ->
-// 219.0), and so do the decoded-fp16 widths (b = 13: 296.0 -> 334.3) and raw
-// fp16 (241.5 -> 254.1), which keep four waves; b <= 6 (not measured) keeps
-// them too.  b = 12 lost with two weight blocks per wave (258.1 -> 262.8)
-// and gains with one (240.8 -> 235.0; see pp_weight_blocks).
+// 14336 x 4096 M = 4096 b = 10 443.0 -> 427.4).  With two weight blocks
+// per wave b = 7 lost (214.3 -> 219.0), and so did b = 12 (258.1 -> 262.8),
+// the decoded-fp16 widths (b = 13: 296.0 -> 334.3) and raw fp16 (241.5 ->
+// 254.1); with one block per wave (pp_weight_blocks) every packed width
+// and arithmetic gains, so only raw fp16 keeps four waves.
 template <int B, int MODE>
 inline bool prefill_eight_waves() {
     const int mode = g_prefill_tiles.load(std::memory_order_relaxed);
     if (mode == kPrefillTilesWide8 || mode == kPrefillTilesWide8Plain || mode == kPrefillTilesWide8Short) return true;
-    return mode == 0 && MODE == kModeQ && B >= 8 && B <= 12;
+    return mode == 0 && MODE != kModeRaw;
 }
 
 // Whether the 256 x 256 prefill tiles finish before the 128 x 256 ones.

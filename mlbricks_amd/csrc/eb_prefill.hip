@@ -16,7 +16,7 @@
 //    The two waves of a column group load and decode the same weight bits
 //    (the second load hits the CU's L1); each wave reads only its own 128
 //    activation rows from LDS;
-//  * one weight block per wave (b = 9..12): wave w owns weight rows
+//  * one weight block per wave (every width but b = 8): wave w owns weight rows
 //    32 w .. 32 w + 31 for all 256 activation rows, 8 x 1 blocks.  Each
 //    weight bit is loaded and decoded once; each wave reads every
 //    activation row from LDS.
@@ -91,10 +91,14 @@ constexpr int ring_depth() {
 // (14336 x 4096 M = 2048 unless stated, us, two blocks -> one): b = 8
 // 202.1 -> 205.5; b = 9 215.0 -> 212.4; b = 10 216.7 -> 215.8; b = 11
 // 248.7 -> 231.5, 4096^2 M = 8192 272.6 -> 251.5; b = 12 250.6 -> 235.0
-// (the four-wave kernel: 240.8).
+// (the four-wave kernel: 240.8).  Against the four-wave kernel, one block
+// per wave also wins where two lost (us, four waves -> eight, one block):
+// b = 3 216.5 -> 206.6, b = 5 220.2 -> 210.9, b = 7 228.2 -> 222.6,
+// decoded fp16 at b = 10 278.2 -> 271.7, b = 13 292.4 -> 279.2, b = 15
+// 307.0 -> 301.7.  Raw fp16 (b = 16) keeps the four-wave kernel.
 template <int B, int MODE>
 constexpr int pp_weight_blocks() {
-    return (MODE == kModeQ && B >= 9 && B <= 12) ? 1 : 2;
+    return (MODE == kModeRaw || (MODE == kModeQ && B == 8)) ? 2 : 1;
 }
 
 // AB: 32-row activation blocks per tile and weight-block column, so 64 AB
