@@ -16,14 +16,14 @@
 //    The two waves of a column group load and decode the same weight bits
 //    (the second load hits the CU's L1); each wave reads only its own 128
 //    activation rows from LDS;
-//  * one weight block per wave (every width but b = 8): wave w owns weight rows
-//    32 w .. 32 w + 31 for all 256 activation rows, 8 x 1 blocks.  Each
-//    weight bit is loaded and decoded once; each wave reads every
+//  * one weight block per wave (every width but b = 8): wave w owns weight
+//    rows 32 w .. 32 w + 31 for all 256 activation rows, 8 x 1 blocks.
+//    Each weight bit is loaded and decoded once; each wave reads every
 //    activation row from LDS.
 //
 // Per K step (128 columns = one plane tile) the CU moves 64 KB of
-// activations global -> LDS and 2 x 40 KB (b = 10) of weight bits global ->
-// registers for 512 MFMAs.
+// activations global -> LDS and 40 KB (b = 10) of weight bits global ->
+// registers, twice that with two weight blocks per wave, for 512 MFMAs.
 //
 // Pipeline, in half steps h (64 columns: group pair h % 2 of step h / 2):
 //  * activations of half step h go to LDS half-stage h % 4 (32 KB; rows of
@@ -31,12 +31,14 @@
 //    rows read by one operand read land on distinct banks); half step h + 2
 //    is loaded during half step h, one 1 KB load per wave and slice;
 //  * weight bits sit in a register ring of D half steps: with D = 3 (b <= 12)
-//    those of h + 2 are loaded in slices 0 and 1 of half step h; with D = 2
+//    those of h + 2 are loaded in slices 0 (and 1, with two weight blocks)
+//    of half step h; with D = 2
 //    (b >= 13 and raw fp16, whose groups are larger) those of h + 1, in
 //    slice 0, ahead of that slice's activation load;
-//  * a slice (16 columns) is two halves of four MFMAs; the A operands of one
-//    half are read from LDS and the B operands of the next slice decoded
-//    while the other half's MFMAs run;
+//  * a slice (16 columns) is two halves of MFMAs (four each with two weight
+//    blocks per wave; AB each with one); the A operands of one half are read
+//    from LDS and the B operands of the next slice decoded while the other
+//    half's MFMAs run;
 //  * one workgroup barrier per half step, before the last slice's second
 //    half: every read of the half-stage being retired has returned and the
 //    next half step's activations and weight bits have landed.
