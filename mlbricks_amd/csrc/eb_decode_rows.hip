@@ -114,7 +114,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) void linear_decode_rows_kernel(
 #pragma unroll
         for (int w = 0; w < kRowsWaves; ++w) v += red[w][r][src][e];
         const float sc = MODE == kModeQ ? m.scales[n] : 1.0f;
-        y[static_cast<size_t>(mi) * m.rows + n] = epilogue<MODE>(v, sc, bias != nullptr, bias ? bias[n] : 0);
+        store_out(y + static_cast<size_t>(mi) * m.rows + n, epilogue<MODE>(v, sc, bias != nullptr, bias ? bias[n] : 0));
     }
 }
 

@@ -230,6 +230,28 @@ __device__ __forceinline__ uint16_t epilogue(float acc, float s, bool has_bias, 
     return y;
 }
 
+// Output store of the decode-shaped kernels: agent scope, so the store writes
+// through this XCD's L2 (global_store_short ... sc1) and leaves no dirty line
+// for the end-of-kernel L2 write-back.  Measured on MI355X (us, plain store
+// -> this): 4096^2 b = 10 M = 1 5.695 -> 5.590, b = 9 5.397 -> 5.310,
+// 4096 x 3072 5.143 -> 5.056; results bit-identical.
+__device__ __forceinline__ void store_out(uint16_t* p, uint16_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// 16-byte output store of the prefill-shaped kernels: nontemporal
+// (global_store_dwordx4 ... nt).  The output is written once and not read
+// back by the kernel, so it streams past the L2 instead of displacing the
+// activation and weight blocks that the workgroups of an XCD share there.
+// Measured on MI355X (eight-wave kernel, b = 10, us, plain store -> this):
+// 14336 x 4096 M = 2048 211-212 -> 203.5, 4096^2 M = 8192 229-231 -> 220.0;
+// results bit-identical.  (For the decode kernels' few output lines a
+// nontemporal store gained nothing: 5.695 -> 5.695 us.)
+__device__ __forceinline__ void store_out16(uint16_t* p, const uint4& v) {
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4*>(p));
+}
+
 // Load the 32 activations x[row][k0 .. k0+32) as four 8-half MFMA operands,
 // zero beyond `cols`.  vec: cols % 8 == 0 and x 16-byte aligned.
 __device__ __forceinline__ void load_x32(const uint16_t* __restrict__ xrow, int k0, int cols, bool vec,

@@ -544,8 +544,8 @@ __global__ __launch_bounds__(64 * WAVES) void linear_decode_kernel(
             for (int w = 0; w < WAVES; ++w) v += red[w][src][e];
             const int mi = 16 * mb + 4 * (src >> 4) + e;   // D[4*(l/16)+e][l%16] of block mb
             if (mi < M && on < m.rows) {
-                y[static_cast<size_t>(mi) * m.rows + on] =
-                    epilogue<MODE>(v, out_scale, bias != nullptr, out_bias);
+                store_out(y + static_cast<size_t>(mi) * m.rows + on,
+                          epilogue<MODE>(v, out_scale, bias != nullptr, out_bias));
             }
         }
     }
@@ -676,7 +676,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void linear_gemv_kernel(
         float v = 0.0f;
 #pragma unroll
         for (int w = 0; w < kGemvWaves; ++w) v += red[w][e][threadIdx.x & 15];
-        y[static_cast<size_t>(e) * m.rows + on] = epilogue<MODE>(v, out_scale, bias != nullptr, out_bias);
+        store_out(y + static_cast<size_t>(e) * m.rows + on, epilogue<MODE>(v, out_scale, bias != nullptr, out_bias));
     }
 }
 
@@ -1199,7 +1199,7 @@ __global__ __launch_bounds__(256 * KS) void linear_prefill_kernel(
             const uint4 v = *reinterpret_cast<const uint4*>(xs + r * kCPitch + chunk * 16);
             uint16_t* dst = y + static_cast<size_t>(gr) * m.rows + gn;
             if (yvec) {
-                *reinterpret_cast<uint4*>(dst) = v;
+                store_out16(dst, v);
             } else {
                 const uint16_t* h = reinterpret_cast<const uint16_t*>(&v);
 #pragma unroll
@@ -1508,7 +1508,7 @@ __global__ __launch_bounds__(256) void linear_prefill_wide_kernel(
             const uint4 v = *reinterpret_cast<const uint4*>(xs + r * kCPitch + chunk * 16);
             uint16_t* dst = y + static_cast<size_t>(gr) * m.rows + gn;
             if (yvec) {
-                *reinterpret_cast<uint4*>(dst) = v;
+                store_out16(dst, v);
             } else {
                 const uint16_t* hh = reinterpret_cast<const uint16_t*>(&v);
 #pragma unroll

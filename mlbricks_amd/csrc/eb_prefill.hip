@@ -400,7 +400,7 @@ __global__ __launch_bounds__(64 * kQWaves) void linear_prefill_pp_kernel(
         const uint4 v = *reinterpret_cast<const uint4*>(xs + r * kQCPitch + chunk * 16);
         uint16_t* dst = y + static_cast<size_t>(gr) * m.rows + gn;
         if (yvec) {
-            *reinterpret_cast<uint4*>(dst) = v;
+            store_out16(dst, v);
         } else {
             const uint16_t* hv = reinterpret_cast<const uint16_t*>(&v);
 #pragma unroll
