@@ -406,6 +406,34 @@ def test_forward_unaligned_activation_pointer(native, M):
     assert _rel_max(y, ref) <= TOL
 
 
+@pytest.mark.parametrize("tiles", ["auto", "wide8", "wide"])
+@pytest.mark.parametrize("M", [1, 16, 64, 300, 1100])
+def test_forward_into_unaligned_output(native, M, tiles):
+    """An output 2 bytes off 16-byte alignment takes the element stores of
+    the prefill kernels; the decode kernels store single elements anyway.
+    Either way the result equals the one written to an aligned output."""
+    rows, cols, b = 512, 512, 10
+    rng = np.random.default_rng(M)
+    q = _codes(rng, rows, cols, b)
+    s = rng.uniform(0.002, 0.05, size=rows).astype(np.float32)
+    m = native.RuntimeMatrix._compressSelectedCodes(q, s, b, 0.01, 0.0)
+    x = _x16(rng, M, cols)
+    bias = torch.from_numpy(rng.standard_normal(rows).astype(np.float16)).cuda()
+    buf = torch.full((M * rows + 1,), float("nan"), dtype=torch.float16, device="cuda")
+    out = buf[1:].view(M, rows)
+    assert out.data_ptr() % 16 != 0
+    native.set_prefill_tiles(tiles)
+    try:
+        ref = m.forwardTorch(x, bias=bias)
+        y = m.forwardTorch(x, out=out, bias=bias)
+        torch.cuda.synchronize()
+    finally:
+        native.set_prefill_tiles("auto")
+    assert y.data_ptr() == out.data_ptr()
+    assert torch.equal(out, ref)
+    assert torch.isnan(buf[0])                      # nothing written before the output
+
+
 @pytest.mark.parametrize("M", [1, 100])
 def test_forward_bias_is_added_like_torch(native, M):
     rows, cols, b = 50, 128, 8
